@@ -1,0 +1,281 @@
+"""Benchmark of the full-attention hot path on one MI355X.
+
+Default workload (the metric's decode half): batch-1
+GQA decode, 24 q heads / 4 kv heads, head_dim 256, 32768 keys of q8_0 K/V
+(N(0,1) plus one x8 outlier dim per head), one step = append-and-quantize of
+the new token's K and V rows at position 32767 + gated split-KV attention over
+keys 0..32767. Inputs are resident in HBM before timing.
+
+value = algorithmic bytes of a step / step time (GB/s). The roofline object
+covers the dominant kernel (the attention launch), timed with HIP events on
+the stream the library launches on. cpu_baseline = the scalar CPU oracle (f64,
+one thread) on the same workload. `--workload prefill` measures BASELINE
+configs[4] instead (TFLOP/s of the causal QK^T + PV flops); `--extra` adds the
+other configs' numbers under "extra".
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
+NH, NKV, HD = 24, 4, 256
+SEED = 20260
+
+
+def pkg():
+    import importlib.util
+    name = "rdna4_infer_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, os.path.join(ROOT, "rdna4-infer_amd", "__init__.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def make_cache(torch, rd4, t, n, seed, outlier):
+    """n rows x 4 kv heads of N(0,1) values (optionally one x8 dim per head),
+    quantized on the GPU by the library's own store kernel."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    rb = rd4.kv_row_bytes(t, HD)
+    cache = torch.empty(n * NKV * rb, dtype=torch.uint8, device="cuda")
+    step = 4096
+    for r0 in range(0, n, step):
+        r1 = min(n, r0 + step)
+        x = torch.randn((r1 - r0, NKV, HD), generator=g, device="cuda", dtype=torch.float32)
+        if outlier:
+            x[:, :, 7] *= 8
+        rd4.kv_store_rows(t, x.reshape(-1), cache[r0 * NKV * rb:r1 * NKV * rb])
+    return cache
+
+
+class Timer:
+    """Pairs of events around the dominant kernel inside the timed loop."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def begin(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.append([e, None])
+
+    def end(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs[-1][1] = e
+
+    def mean_ms(self):
+        return float(np.mean([a.elapsed_time(b) for a, b in self.pairs]))
+
+
+def decode_workload(torch, rd4, kt, ctx, outlier, gated=True):
+    """Returns (step_fn(timer), algorithmic step bytes, dominant-kernel bytes, cpu_fn, info)."""
+    pos = ctx - 1
+    rb = rd4.kv_row_bytes(kt, HD)
+    kc = make_cache(torch, rd4, kt, ctx, SEED, outlier)
+    vc = make_cache(torch, rd4, kt, ctx, SEED + 1, outlier)
+    g = torch.Generator(device="cuda").manual_seed(SEED + 2)
+    q = torch.randn(NH * HD, generator=g, device="cuda")
+    gate0 = torch.randn(NH * HD, generator=g, device="cuda")
+    gate = gate0.clone()
+    krow = torch.randn(NKV * HD, generator=g, device="cuda")
+    vrow = torch.randn(NKV * HD, generator=g, device="cuda")
+    out = torch.empty(NH * HD, device="cuda")
+    scale = 1.0 / np.sqrt(HD)
+    kslot = kc[pos * NKV * rb:(pos + 1) * NKV * rb]
+    vslot = vc[pos * NKV * rb:(pos + 1) * NKV * rb]
+
+    def step(timer=None):
+        rd4.kv_store_rows(kt, krow, kslot)
+        rd4.kv_store_rows(kt, vrow, vslot)
+        if timer:
+            timer.begin()
+        rd4.attn_decode(q, kc, vc, out, pos, NH, NKV, HD, scale, kt, kt, gate=gate if gated else None)
+        if timer:
+            timer.end()
+
+    kv_bytes = ctx * NKV * 2 * rb
+    small = NH * HD * 4 * (4 if gated else 2)  # q, out (+ gate read and write)
+    append = 2 * NKV * HD * 4 + 2 * NKV * rb
+    attn_bytes = kv_bytes + small
+    step_bytes = attn_bytes + append
+
+    def cpu(budget_s=12.0):
+        """Scalar f64 oracle on the same cache, repeated for ~budget_s; returns GB/s."""
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        kh, vh = kc.cpu().numpy(), vc.cpu().numpy()
+        qh = q.cpu().numpy()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            orc.attn_decode(qh, kh, vh, pos, NH, NKV, HD, scale, kt, kt)
+            reps += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        dt = (time.perf_counter() - t0) / reps
+        return attn_bytes / dt / 1e9, "full decode step over %d keys x %d reps" % (ctx, reps)
+
+    info = {"workload": "decode", "kv_type": rd4.TYPE_NAMES[kt], "ctx": ctx, "n_head": NH,
+            "n_head_kv": NKV, "head_dim": HD, "gate": gated, "append": True, "seed": SEED}
+    return step, step_bytes, attn_bytes, cpu, info
+
+
+def prefill_workload(torch, rd4, n_prefix=4096, n_q=4096):
+    """4096 f16 queries at positions 4096..8191 over an f16 cache of
+    8192 rows (prefix + the chunk), causal, gated; the chunk's K/V rows are also
+    appended to a q8_0 cache in the same step."""
+    ktot = n_prefix + n_q
+    kc = make_cache(torch, rd4, 1, ktot, SEED, False)
+    vc = make_cache(torch, rd4, 1, ktot, SEED + 1, False)
+    g = torch.Generator(device="cuda").manual_seed(SEED + 3)
+    q = torch.randn((n_q, NH, HD), generator=g, device="cuda").half()
+    gate = torch.randn((n_q, NH, HD), generator=g, device="cuda")
+    knew = torch.randn(n_q * NKV * HD, generator=g, device="cuda")
+    vnew = torch.randn(n_q * NKV * HD, generator=g, device="cuda")
+    rb8 = rd4.kv_row_bytes(2, HD)
+    kq8 = torch.empty(ktot * NKV * rb8, dtype=torch.uint8, device="cuda")
+    vq8 = torch.empty_like(kq8)
+    out = torch.empty((n_q, NH, HD), device="cuda")
+    pairs = n_q * (n_prefix + 1) + n_q * (n_q - 1) // 2
+    flops = NH * pairs * 4 * HD
+
+    def step(timer=None):
+        rd4.kv_store_rows(2, knew, kq8[n_prefix * NKV * rb8:])
+        rd4.kv_store_rows(2, vnew, vq8[n_prefix * NKV * rb8:])
+        if timer:
+            timer.begin()
+        rd4.prefill(q, kc, vc, out, n_prefix, NH, NKV, HD, 1.0 / 16, 1, 1, gate=gate)
+        if timer:
+            timer.end()
+
+    def cpu(budget_s=12.0):
+        """Oracle on a deterministic subset of query rows, scaled by causal pairs."""
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        kh, vh = kc.cpu().numpy(), vc.cpu().numpy()
+        qh = q.float().cpu().numpy()
+        rows = [0, n_q // 3, 2 * n_q // 3, n_q - 1]
+        t0 = time.perf_counter()
+        done_pairs = 0
+        i = 0
+        while time.perf_counter() - t0 < budget_s:
+            r = rows[i % len(rows)]
+            orc.attn_batch(qh[r:r + 1], kh, vh, [n_prefix + r], NH, NKV, HD, 1 / 16, 1, 1)
+            done_pairs += n_prefix + r + 1
+            i += 1
+        dt = time.perf_counter() - t0
+        return NH * done_pairs * 4 * HD / dt / 1e12, "%d query rows of the chunk, scaled by causal pairs" % i
+
+    info = {"workload": "prefill", "kv_type": "f16", "q_type": "f16", "n_prefix": n_prefix,
+            "n_q": n_q, "n_head": NH, "n_head_kv": NKV, "head_dim": HD, "causal": True,
+            "gate": True, "append": "q8_0", "seed": SEED}
+    return step, flops, flops, cpu, info
+
+
+def measure(torch, step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = Timer(torch)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(timer)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    return wall_ms, timer.mean_ms()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="decode_q8_0",
+                    choices=["decode_q8_0", "decode_f16", "decode_q4_0", "prefill"])
+    ap.add_argument("--extra", action="store_true", help="also measure the other configs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the decode would shard "
+              "by key ranges with an LSE all-gather; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    rd4 = pkg()
+    rd4.lib()
+    if rd4.lib().rd4_init() != 0:
+        raise SystemExit("rd4_init failed: " + rd4.lib().rd4_last_error().decode())
+
+    def build(name):
+        if name == "decode_q8_0":
+            return decode_workload(torch, rd4, 2, 32768, True)
+        if name == "decode_f16":
+            return decode_workload(torch, rd4, 1, 32768, False)
+        if name == "decode_q4_0":
+            return decode_workload(torch, rd4, 3, 131001, False)
+        return prefill_workload(torch, rd4)
+
+    step, step_units, dom_units, cpu, info = build(args.workload)
+    wall_ms, dom_ms = measure(torch, step, args.steps, args.warmup)
+    is_prefill = args.workload == "prefill"
+    if is_prefill:
+        metric, unit = "prefill attn TFLOP/s @4K causal", "TFLOP/s"
+        value = step_units / (wall_ms * 1e-3) / 1e12
+        achieved = dom_units / (dom_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": F16_MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / F16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "kernel_ms": round(dom_ms, 4)}
+        dtype = "f16"
+    else:
+        metric, unit = "attn decode KV GB/s @32K ctx (q8_0 KV)", "GB/s"
+        if args.workload != "decode_q8_0":
+            metric = "attn decode KV GB/s (%s, %d keys)" % (info["kv_type"], info["ctx"])
+        value = step_units / (wall_ms * 1e-3) / 1e9
+        achieved = dom_units / (dom_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel_us": round(dom_ms * 1e3, 3)}
+        info["us_per_token_layer"] = round(wall_ms * 1e3, 3)
+        dtype = "f32"
+    res = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 5),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+           "data": "synthetic (seeded N(0,1), random K/V/Q/gate)", "config": info,
+           "roofline": roof}
+    if not args.no_cpu:
+        v, sample = cpu()
+        res["cpu_baseline"] = {"value": round(v, 4), "unit": unit, "cores": 1, "kind": "port",
+                               "sample": sample + " (oracle/oracle.c, f64 accumulate)",
+                               "host_nproc": os.cpu_count()}
+    if args.extra:
+        res["extra"] = {}
+        for name in ("decode_f16", "decode_q4_0", "prefill"):
+            if name == args.workload:
+                continue
+            st, su, du, _, inf = build(name)
+            w, d = measure(torch, st, 5 if name == "prefill" else 50, 3)
+            if name == "prefill":
+                res["extra"][name] = {"TFLOP/s": round(su / (w * 1e-3) / 1e12, 2),
+                                      "kernel_TFLOP/s": round(du / (d * 1e-3) / 1e12, 2),
+                                      "frac_of_mfma_peak": round(du / (d * 1e-3) / 1e12 / F16_MFMA_PEAK_TFLOPS, 4),
+                                      "ms_per_step": round(w, 4)}
+            else:
+                res["extra"][name] = {"GB/s": round(su / (w * 1e-3) / 1e9, 1),
+                                      "kernel_GB/s": round(du / (d * 1e-3) / 1e9, 1),
+                                      "frac_of_hbm_peak": round(du / (d * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "us_per_token_layer": round(w * 1e3, 2)}
+            del st
+            torch.cuda.empty_cache()
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,167 @@
+/*
+ * rdna4attn -- C ABI of the gfx950 (MI355X) full-attention library.
+ *
+ * Drop-in boundary for rdna4-infer's attention/KV operator API: every entry
+ * point below replaces one `inline` launcher of the reference's headers
+ * (cited per function, file:line into Vmarcelo49/rdna4-infer). The C++ header
+ * shims in include/rdna4/ keep the reference's `rdna4::` names and signatures
+ * and forward here, so graph.cuh / mtp.cuh / main.hip compile unchanged.
+ *
+ * Conventions (same as the reference):
+ *   - all pointers are device pointers unless stated; the caller owns them;
+ *   - work is enqueued on `stream` (a hipStream_t, NULL = the null stream) and
+ *     never synchronised inside the library;
+ *   - KV cache rows are addressed base + (j * n_head_kv + kvh) * row_bytes;
+ *   - keys 0..t are attended (inclusive); t < 0 means no keys -> zeros;
+ *   - query head h reads kv head h / (n_head / n_head_kv);
+ *   - q and out may be the same buffer (in-place).
+ * Return value: RD4_OK (0) on success, a negative RD4_E* code otherwise (the
+ * reference's `false`). Nothing throws and nothing aborts, except the KV table
+ * queries of the C++ shim, which abort on a value outside the enum like the
+ * reference's kv_unreachable() (kv.h:58-69).
+ */
+#ifndef RDNA4ATTN_H
+#define RDNA4ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* KvType values, never renumbered (kv.h:89-98). */
+enum {
+  RD4_KV_F32 = 0,
+  RD4_KV_F16 = 1,
+  RD4_KV_Q8_0 = 2,
+  RD4_KV_Q4_0 = 3,
+  RD4_KV_Q5_0 = 4,
+  RD4_KV_Q4_1 = 5
+};
+
+enum {
+  RD4_OK = 0,
+  RD4_EINVAL = -1,  /* bad shape, head_dim, split count or pointer alignment */
+  RD4_ETYPE = -2,   /* KvType outside the enum */
+  RD4_ELAUNCH = -3, /* HIP reported an error when the kernel was enqueued */
+  RD4_ENOMEM = -4   /* library scratch could not be created */
+};
+
+/* ---- library ------------------------------------------------------------ */
+
+/* Version string of this build. */
+const char *rd4_version(void);
+/* Create the per-device scratch (split-KV partials + merge counters) for the
+ * current device. Called implicitly by the first attention launch on a device;
+ * call it at init to keep allocation out of the first step. No counterpart in
+ * the reference (its graph owned the partial buffer, graph.cuh:771-778). */
+int rd4_init(void);
+/* Human-readable reason of the last non-OK return on this thread. */
+const char *rd4_last_error(void);
+
+/* ---- KV tables (kv.h:100-169) -------------------------------------------- */
+
+/* kv_type_name (kv.h:100): "<unknown-kv-type>" outside the enum. */
+const char *rd4_kv_type_name(int type);
+/* kv_type_parse (kv.h:129): NULL and *out set on success, else the message. */
+const char *rd4_kv_type_parse(const char *name, int *out);
+/* kv_bytes_per_elem (kv.h:139): 0.0 outside the enum. */
+double rd4_kv_bytes_per_elem(int type);
+/* kv_row_bytes (kv.h:155): bytes of one head_dim row; -1 outside the enum. */
+int64_t rd4_kv_row_bytes(int type, int head_dim);
+
+/* ---- KV append / fill / dequant (kv.h:386-694) --------------------------- */
+
+/* kv_store_row_launch (kv.h:683): quantize `width` contiguous f32 values into
+ * the cache bytes at dst (block-local, so width may span n_tok*n_head_kv*hd).
+ * Quantized types need width % 32 == 0; src 4-byte and dst 2-byte aligned. */
+int rd4_kv_store_row_launch(int type, const float *src, void *dst, int64_t width, void *stream);
+/* kv_fill_launch (kv.h:632): fill n_rows rows with the seeded kv_rand hash
+ * (kv.h:508-513), byte-identical to storing those hash values with
+ * rd4_kv_store_row_launch. */
+int rd4_kv_fill_launch(int type, void *cache, int64_t n_rows, int head_dim, uint32_t seed,
+                       void *stream);
+/* Dequantize `width` stored values to f32, as kv_load<>/kv_load8<>
+ * (kv.h:174-368) return them. Test and inspection hook. */
+int rd4_kv_load_rows_launch(int type, const void *src, float *dst, int64_t width, void *stream);
+
+/* ---- decode attention (attn.cuh:200-249, 592-667, 895-956) --------------- */
+
+/* attn_launch (attn.cuh:200): one query token [n_head][head_dim] f32. */
+int rd4_attn_launch(const float *q, const void *k, const void *v, float *out, int t, int n_head,
+                    int n_head_kv, int head_dim, float scale, int kt, int vt, void *stream);
+/* attn_launch_split (attn.cuh:903). `partial` is accepted for source
+ * compatibility and left untouched: the library keeps its partials in its own
+ * scratch. n_splits >= 1 is the minimum key split count. */
+int rd4_attn_launch_split(const float *q, const void *k, const void *v, float *out,
+                          float *partial, int t, int n_head, int n_head_kv, int head_dim,
+                          float scale, int kt, int vt, int n_splits, void *stream);
+/* attn_launch_split_wpb (attn.cuh:630): wpb must be 8, 16 or 32 (bench knob of
+ * the reference; the gfx950 kernels fix their own CTA shape). */
+int rd4_attn_launch_split_wpb(const float *q, const void *k, const void *v, float *out,
+                              float *partial, int t, int n_head, int n_head_kv, int head_dim,
+                              float scale, int kt, int vt, int n_splits, int wpb, void *stream);
+/* attn_partial_bytes (attn.cuh:665). */
+size_t rd4_attn_partial_bytes(int n_head, int head_dim, int n_splits);
+/* attn_split_wpb (attn.cuh:895): the reference's policy values (16 or 8). */
+int rd4_attn_split_wpb(int n_splits);
+
+/* Native decode entry: attention of one token and, when gate != NULL, the
+ * sigmoid output gate fused into the epilogue (out *= sigmoid(gate) and gate <-
+ * sigmoid(gate), the pair attn_launch_split + sigmoid_gate_launch of
+ * graph.cuh:958-981). n_splits = 0 picks the split count for the GPU; n_splits
+ * >= 1 forces exactly that many contiguous key splits. */
+int rd4_attn_decode(const float *q, const void *k, const void *v, float *out, float *gate, int t,
+                    int n_head, int n_head_kv, int head_dim, float scale, int kt, int vt,
+                    int n_splits, void *stream);
+
+/* ---- batched attention (attn.cuh:373-424, 958-1049) ---------------------- */
+
+/* attn_batch_launch (attn.cuh:373): token i of n_tok attends keys 0..pos[i]
+ * (pos is a device int array); q/out [n_tok][n_head][head_dim]. */
+int rd4_attn_batch_launch(const float *q, const void *k, const void *v, float *out,
+                          const int *pos, int n_tok, int n_head, int n_head_kv, int head_dim,
+                          float scale, int kt, int vt, void *stream);
+/* attn_split_batch_launch (attn.cuh:958): as above with n_splits key splits
+ * per token; `partial` accepted and unused as in rd4_attn_launch_split. */
+int rd4_attn_split_batch_launch(const float *q, const void *k, const void *v, float *out,
+                                float *partial, const int *pos, int n_tok, int n_head,
+                                int n_head_kv, int head_dim, float scale, int kt, int vt,
+                                int n_splits, void *stream);
+
+/* ---- prefill (attn_fa2.cuh:173-207) --------------------------------------- */
+
+/* fa2_prefill_launch (attn_fa2.cuh:173): causal prefill of n_q query tokens at
+ * positions pos[i] (device array) over an f16 K/V cache; q/o f32
+ * [n_q][n_head][head_dim]; keys 0..min(pos[i], kmax); keys_total rows exist. */
+int rd4_fa2_prefill_launch(const float *q, const void *k, const void *v, float *o,
+                           const int *pos, int n_q, int kmax, int keys_total, int n_head,
+                           int n_head_kv, int head_dim, float scale, void *stream);
+/* fa2_prefill_usable (attn_fa2.cuh:192): 1 when rd4_fa2_prefill_launch takes
+ * this shape. The gfx950 kernel admits every chunk size and key count for
+ * f16/f16 with head_dim 256 (RD_GFX12_FA2_PREFILL=0 still disables it). */
+int rd4_fa2_prefill_usable(int kt, int vt, int n_q, int pos0, int n_head, int n_head_kv,
+                           int head_dim);
+
+/* Native prefill entry: n_q query tokens at consecutive positions pos0..pos0+n_q-1
+ * attend causally to cache rows 0..pos0+i. q_f16 != 0 means q is f16
+ * [n_q][n_head][hd], else f32. gate (optional, f32, same shape) is fused:
+ * out *= sigmoid(gate), gate <- sigmoid(gate) (graph.cuh:1534-1535). */
+int rd4_prefill(const void *q, int q_f16, const void *k, const void *v, float *out, float *gate,
+                int pos0, int n_q, int n_head, int n_head_kv, int head_dim, float scale, int kt,
+                int vt, void *stream);
+
+/* ---- gate / rope ---------------------------------------------------------- */
+
+/* sigmoid_gate_launch (nn.cuh:414): g <- sigmoid(g); y <- y * g. */
+int rd4_sigmoid_gate_launch(float *g_io, float *y_io, int64_t n, void *stream);
+/* rope_launch (attn.cuh:56): split-half RoPE over the first n_rot dims of each
+ * head of x [n_tokens][n_heads][head_dim], positions pos[t] (device). */
+int rd4_rope_launch(float *x, int n_tokens, int n_heads, int head_dim, int n_rot,
+                    float freq_base, const int *pos, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

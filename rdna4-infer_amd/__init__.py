@@ -1,0 +1,184 @@
+"""Python host side of the gfx950 full-attention library.
+
+Thin ctypes mirror of the C ABI in include/rdna4attn.h, which itself mirrors the
+reference's operator API (include/rdna4/attn.cuh, attn_fa2.cuh, kv.h, nn.cuh of
+Vmarcelo49/rdna4-infer). Functions take torch tensors on the GPU for device
+memory and streams; every call runs the HIP kernels of librdna4attn.so. There is
+no CPU fallback: when the library is missing, loading fails with an error.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librdna4attn.so")
+
+F32, F16, Q8_0, Q4_0, Q5_0, Q4_1 = range(6)
+TYPE_NAMES = ("f32", "f16", "q8_0", "q4_0", "q5_0", "q4_1")
+OK, EINVAL, ETYPE, ELAUNCH, ENOMEM = 0, -1, -2, -3, -4
+
+# exported symbol -> (argtypes, restype); the C-ABI test checks include/ against this
+_P, _I, _I64, _F, _U32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_uint32
+SIGNATURES = {
+    "rd4_version": ([], ctypes.c_char_p),
+    "rd4_init": ([], _I),
+    "rd4_last_error": ([], ctypes.c_char_p),
+    "rd4_kv_type_name": ([_I], ctypes.c_char_p),
+    "rd4_kv_type_parse": ([ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)], ctypes.c_char_p),
+    "rd4_kv_bytes_per_elem": ([_I], ctypes.c_double),
+    "rd4_kv_row_bytes": ([_I, _I], _I64),
+    "rd4_kv_store_row_launch": ([_I, _P, _P, _I64, _P], _I),
+    "rd4_kv_fill_launch": ([_I, _P, _I64, _I, _U32, _P], _I),
+    "rd4_kv_load_rows_launch": ([_I, _P, _P, _I64, _P], _I),
+    "rd4_attn_launch": ([_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P], _I),
+    "rd4_attn_launch_split": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
+    "rd4_attn_launch_split_wpb": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _I, _P], _I),
+    "rd4_attn_partial_bytes": ([_I, _I, _I], ctypes.c_size_t),
+    "rd4_attn_split_wpb": ([_I], _I),
+    "rd4_attn_decode": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
+    "rd4_attn_batch_launch": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P], _I),
+    "rd4_attn_split_batch_launch": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
+    "rd4_fa2_prefill_launch": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
+    "rd4_fa2_prefill_usable": ([_I, _I, _I, _I, _I, _I, _I], _I),
+    "rd4_prefill": ([_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I),
+    "rd4_sigmoid_gate_launch": ([_P, _P, _I64, _P], _I),
+    "rd4_rope_launch": ([_P, _I, _I, _I, _I, _F, _P, _P], _I),
+}
+
+_lib = None
+
+
+class Rd4Error(RuntimeError):
+    pass
+
+
+def lib():
+    """Load librdna4attn.so (built by rdna4-infer_amd/build.py)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise Rd4Error("librdna4attn.so is not built: run rdna4-infer_amd/build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def build():
+    from importlib import util
+    spec = util.spec_from_file_location("_rd4_build", os.path.join(HERE, "build.py"))
+    mod = util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.build(verbose=False)
+
+
+def _check(rc, what):
+    if rc != OK:
+        msg = lib().rd4_last_error().decode()
+        raise Rd4Error("%s failed (%d): %s" % (what, rc, msg))
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+# ---- KV tables (kv.h:100-169) ------------------------------------------------
+
+def kv_type_name(t):
+    return lib().rd4_kv_type_name(t).decode()
+
+
+def kv_type_parse(name):
+    """Returns the KvType value; raises ValueError with the reference's message."""
+    out = ctypes.c_int(-1)
+    err = lib().rd4_kv_type_parse(name.encode(), ctypes.byref(out))
+    if err is not None:
+        raise ValueError(err.decode())
+    return out.value
+
+
+def kv_row_bytes(t, head_dim):
+    return int(lib().rd4_kv_row_bytes(t, head_dim))
+
+
+def kv_bytes_per_elem(t):
+    return float(lib().rd4_kv_bytes_per_elem(t))
+
+
+# ---- KV append / fill / dequant (kv.h:386-694) --------------------------------
+
+def kv_store_rows(t, src, dst, width=None):
+    """kv_store_row_launch: quantize f32 `src` into uint8 tensor `dst`."""
+    width = src.numel() if width is None else width
+    _check(lib().rd4_kv_store_row_launch(t, _ptr(src), _ptr(dst), width, _stream()), "kv_store")
+
+
+def kv_fill(t, cache, n_rows, head_dim, seed):
+    _check(lib().rd4_kv_fill_launch(t, _ptr(cache), n_rows, head_dim, seed & 0xFFFFFFFF, _stream()),
+           "kv_fill")
+
+
+def kv_load_rows(t, src, dst, width):
+    _check(lib().rd4_kv_load_rows_launch(t, _ptr(src), _ptr(dst), width, _stream()), "kv_load")
+
+
+# ---- attention -----------------------------------------------------------------
+
+def attn_decode(q, k, v, out, t, n_head, n_head_kv, head_dim, scale, kt, vt, gate=None, n_splits=0):
+    _check(lib().rd4_attn_decode(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(gate), t, n_head,
+                                 n_head_kv, head_dim, scale, kt, vt, n_splits, _stream()),
+           "attn_decode")
+
+
+def attn_launch(q, k, v, out, t, n_head, n_head_kv, head_dim, scale, kt, vt):
+    _check(lib().rd4_attn_launch(_ptr(q), _ptr(k), _ptr(v), _ptr(out), t, n_head, n_head_kv,
+                                 head_dim, scale, kt, vt, _stream()), "attn_launch")
+
+
+def attn_launch_split(q, k, v, out, partial, t, n_head, n_head_kv, head_dim, scale, kt, vt, n_splits):
+    _check(lib().rd4_attn_launch_split(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(partial), t,
+                                       n_head, n_head_kv, head_dim, scale, kt, vt, n_splits,
+                                       _stream()), "attn_launch_split")
+
+
+def attn_batch(q, k, v, out, pos, n_head, n_head_kv, head_dim, scale, kt, vt):
+    _check(lib().rd4_attn_batch_launch(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(pos), pos.numel(),
+                                       n_head, n_head_kv, head_dim, scale, kt, vt, _stream()),
+           "attn_batch")
+
+
+def attn_split_batch(q, k, v, out, pos, n_head, n_head_kv, head_dim, scale, kt, vt, n_splits):
+    _check(lib().rd4_attn_split_batch_launch(_ptr(q), _ptr(k), _ptr(v), _ptr(out), None, _ptr(pos),
+                                             pos.numel(), n_head, n_head_kv, head_dim, scale, kt,
+                                             vt, n_splits, _stream()), "attn_split_batch")
+
+
+def prefill(q, k, v, out, pos0, n_head, n_head_kv, head_dim, scale, kt, vt, gate=None):
+    """Causal prefill of q.shape[0] tokens at positions pos0.. (f16 or f32 q)."""
+    import torch
+    q_f16 = 1 if q.dtype == torch.float16 else 0
+    _check(lib().rd4_prefill(_ptr(q), q_f16, _ptr(k), _ptr(v), _ptr(out), _ptr(gate), pos0,
+                             q.shape[0], n_head, n_head_kv, head_dim, scale, kt, vt, _stream()),
+           "prefill")
+
+
+def fa2_prefill(q, k, v, out, pos, kmax, keys_total, n_head, n_head_kv, head_dim, scale):
+    _check(lib().rd4_fa2_prefill_launch(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(pos), pos.numel(),
+                                        kmax, keys_total, n_head, n_head_kv, head_dim, scale,
+                                        _stream()), "fa2_prefill")
+
+
+def sigmoid_gate(g, y):
+    _check(lib().rd4_sigmoid_gate_launch(_ptr(g), _ptr(y), g.numel(), _stream()), "sigmoid_gate")
+
+
+def rope(x, n_tokens, n_heads, head_dim, n_rot, freq_base, pos):
+    _check(lib().rd4_rope_launch(_ptr(x), n_tokens, n_heads, head_dim, n_rot, freq_base, _ptr(pos),
+                                 _stream()), "rope")

@@ -1,0 +1,47 @@
+"""Build librdna4attn.so for gfx950 in-tree with hipcc (no torch extension).
+
+Usage: python rdna4-infer_amd/build.py   (also called by __graft_entry__.build()).
+"""
+import concurrent.futures
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "librdna4attn.so")
+SOURCES = ["kv.hip", "attn_generic.hip", "prefill.hip", "misc.hip", "capi.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+    # packed FP32 instructions are kept out of every code object
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _compile(src):
+    obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
+    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    msgs = [l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l]
+    return src, r.returncode, obj, "\n".join(msgs)
+
+
+def build(verbose=True):
+    os.makedirs(OBJ, exist_ok=True)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
+        results = list(ex.map(_compile, SOURCES))
+    bad = [r for r in results if r[1] != 0]
+    for src, rc, _, msg in results:
+        if msg.strip() and (verbose or rc):
+            print("[%s]\n%s" % (src, msg), file=sys.stderr)
+    if bad:
+        raise RuntimeError("hipcc failed for: " + ", ".join(b[0] for b in bad))
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB] + [r[2] for r in results]
+    subprocess.run(cmd, check=True)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build())

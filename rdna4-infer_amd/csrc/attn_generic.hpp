@@ -1,0 +1,33 @@
+// Internal interface of the attention kernels (not part of the C ABI).
+#pragma once
+#include "common.hpp"
+
+namespace rd4 {
+
+// Split count ceiling of the library's partial scratch per (token, head).
+constexpr int kMaxSplits = 256;
+
+struct AttnArgs {
+  const float *q;         // [n_tok][n_head][hd] f32 (or f16 when q_f16)
+  int q_f16;
+  const uint8_t *k;       // cache rows [pos][n_head_kv][row]
+  const uint8_t *v;
+  float *out;             // [n_tok][n_head][hd] f32 (may alias q)
+  float *gate;            // optional [n_tok][n_head][hd]: in logits, out sigmoid
+  const int *pos;         // device positions per token, or nullptr -> t
+  int t;                  // last key index for the single-token launch
+  int n_head, n_head_kv, head_dim;
+  float scale;
+  int n_splits;           // key splits per (token, kv head)
+  float *partial;         // [n_tok][n_head][n_splits][2 + hd] scratch
+  int64_t l1_offset;      // floats from partial to the level-1 merge records
+  unsigned *counters;     // [n_tok][n_head_kv][n_chunks][kCtrStride], zero between launches
+  // filled by the launcher
+  int n_chunks;
+  int k_lds_stride, v_lds_stride;
+};
+
+hipError_t attn_generic_launch(int kt, int vt, AttnArgs a, int n_tok, hipStream_t st);
+size_t generic_lds_bytes(int kt, int vt, int hd, int n_splits);
+
+}  // namespace rd4

@@ -1,0 +1,347 @@
+// C ABI of the gfx950 full-attention library (declared in include/rdna4attn.h).
+//
+// Validation, split policy, per-device scratch and dispatch to the kernels. The
+// reference's launchers (include/rdna4/attn.cuh, attn_fa2.cuh, kv.h, nn.cuh)
+// return false for an unsupported shape or a launch error; these return a
+// negative RD4_E* code in the same cases.
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/rdna4attn.h"
+#include "merge.hpp"
+#include "prefill.hpp"
+
+namespace rd4 {
+hipError_t kv_store_launch(int t, const float *src, uint8_t *dst, int64_t width, hipStream_t st);
+hipError_t kv_fill_launch(int t, uint8_t *dst, int64_t n, uint32_t seed, hipStream_t st);
+hipError_t kv_load_launch(int t, const uint8_t *src, float *dst, int64_t n, hipStream_t st);
+hipError_t sigmoid_gate_launch(float *g, float *y, int64_t n, hipStream_t st);
+hipError_t rope_launch(float *x, int n_tokens, int n_heads, int head_dim, int n_rot,
+                       float freq_base, const int *pos, hipStream_t st);
+}  // namespace rd4
+
+using namespace rd4;
+
+namespace {
+
+thread_local char g_err[256] = "";
+
+int fail(int code, const char *fmt, const char *detail = "") {
+  std::snprintf(g_err, sizeof(g_err), fmt, detail);
+  return code;
+}
+
+int launched(hipError_t e, const char *what) {
+  if (e == hipSuccess) return RD4_OK;
+  std::snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
+  return RD4_ELAUNCH;
+}
+
+bool valid_type(int t) { return t >= 0 && t < kNumTypes; }
+
+// Per-device scratch: split partials (level 0 and level 1) and merge counters.
+// Sized once; a launch that would not fit uses fewer splits.
+constexpr int kMaxDevices = 64;
+constexpr int64_t kPartialFloats = 16ll << 20;  // 64 MiB
+constexpr int64_t kCounterWords = 1 << 20;
+struct Scratch {
+  float *partial = nullptr;
+  unsigned *counters = nullptr;
+};
+Scratch g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int get_scratch(Scratch **out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(RD4_EINVAL, "no current HIP device%s");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  Scratch &s = g_scratch[dev];
+  if (!s.partial) {
+    if (hipMalloc(&s.partial, kPartialFloats * sizeof(float)) != hipSuccess)
+      return fail(RD4_ENOMEM, "scratch allocation failed%s");
+    if (hipMalloc(&s.counters, kCounterWords * sizeof(unsigned)) != hipSuccess ||
+        hipMemset(s.counters, 0, kCounterWords * sizeof(unsigned)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+      (void)hipFree(s.partial);
+      s.partial = nullptr;
+      return fail(RD4_ENOMEM, "counter allocation failed%s");
+    }
+  }
+  *out = &s;
+  return RD4_OK;
+}
+
+int check_attn_shape(int n_head, int n_head_kv, int head_dim, int kt, int vt) {
+  if (!valid_type(kt) || !valid_type(vt)) return fail(RD4_ETYPE, "KvType outside the enum%s");
+  if (head_dim <= 0 || head_dim % 32 != 0 || head_dim / 32 > 16)
+    return fail(RD4_EINVAL, "head_dim must be a multiple of 32, at most 512%s");
+  if (n_head_kv <= 0 || n_head <= 0 || n_head % n_head_kv != 0)
+    return fail(RD4_EINVAL, "n_head must be a positive multiple of n_head_kv%s");
+  return RD4_OK;
+}
+
+// Splits the GPU wants for `keys` keys of one token: enough CTAs to give every
+// CU several, while keeping at least two 32-key tiles per split.
+int auto_splits(int keys, int ctas_per_split) {
+  if (keys <= 64) return 1;
+  int s = (1024 + ctas_per_split - 1) / ctas_per_split;
+  const int by_keys = (keys + 63) / 64;
+  if (s > by_keys) s = by_keys;
+  if (s > kMaxSplits) s = kMaxSplits;
+  return s < 1 ? 1 : s;
+}
+
+// Common body of every decode-style launch.
+int run_attn(const float *q, const void *k, const void *v, float *out, float *gate,
+             const int *pos, int t, int n_tok, int n_head, int n_head_kv, int head_dim,
+             float scale, int kt, int vt, int splits, hipStream_t st) {
+  int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
+  if (rc) return rc;
+  if (n_tok < 1) return fail(RD4_EINVAL, "n_tok must be >= 1%s");
+  if (!q || !k || !v || !out) return fail(RD4_EINVAL, "null buffer%s");
+  const int n_chunks = (n_head / n_head_kv + 7) / 8;
+  const int64_t rec = 2 + head_dim;
+  if (splits < 1) splits = 1;
+  if (splits > kMaxSplits) splits = kMaxSplits;
+  AttnArgs a{};
+  a.q = q;
+  a.k = (const uint8_t *)k;
+  a.v = (const uint8_t *)v;
+  a.out = out;
+  a.gate = gate;
+  a.pos = pos;
+  a.t = t;
+  a.n_head = n_head;
+  a.n_head_kv = n_head_kv;
+  a.head_dim = head_dim;
+  a.scale = scale;
+  if (splits > 1) {
+    Scratch *s = nullptr;
+    if ((rc = get_scratch(&s))) return rc;
+    // level-0 + level-1 records must fit; counters too.
+    auto floats_for = [&](int S) {
+      const int NG = (S + kMergeFan - 1) / kMergeFan;
+      return (int64_t)n_tok * n_head * rec * (S + (NG > 1 ? NG : 0));
+    };
+    while (splits > 1 && floats_for(splits) > kPartialFloats) splits = (splits + 1) / 2;
+    const int64_t ctr_words = (int64_t)n_tok * n_head_kv * n_chunks * kCtrStride;
+    if (ctr_words > kCounterWords) splits = 1;
+    a.partial = s->partial;
+    a.counters = s->counters;
+    a.l1_offset = (int64_t)n_tok * n_head * splits * rec;
+  }
+  a.n_splits = splits;
+  if (decode_mfma_supported(kt, vt, n_head, n_head_kv, head_dim))
+    return launched(decode_mfma_launch(kt, vt, a, n_tok, st), "decode kernel");
+  return launched(attn_generic_launch(kt, vt, a, n_tok, st), "attention kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *rd4_version(void) { return "rdna4attn-gfx950 0.1"; }
+
+int rd4_init(void) {
+  Scratch *s = nullptr;
+  return get_scratch(&s);
+}
+
+const char *rd4_last_error(void) { return g_err; }
+
+const char *rd4_kv_type_name(int type) {
+  static const char *names[] = {"f32", "f16", "q8_0", "q4_0", "q5_0", "q4_1"};
+  return valid_type(type) ? names[type] : "<unknown-kv-type>";
+}
+
+const char *rd4_kv_type_parse(const char *name, int *out) {
+  for (int t = 0; t < kNumTypes; ++t) {
+    if (name && std::strcmp(name, rd4_kv_type_name(t)) == 0) {
+      if (out) *out = t;
+      return nullptr;
+    }
+  }
+  return "kv type must be one of f32, f16, q8_0, q4_0, q5_0, q4_1";
+}
+
+double rd4_kv_bytes_per_elem(int type) {
+  if (!valid_type(type)) return 0.0;
+  if (type == RD4_KV_F32) return 4.0;
+  if (type == RD4_KV_F16) return 2.0;
+  return block_bytes(type) / 32.0;
+}
+
+int64_t rd4_kv_row_bytes(int type, int head_dim) { return row_bytes(type, head_dim); }
+
+int rd4_kv_store_row_launch(int type, const float *src, void *dst, int64_t width, void *stream) {
+  if (!valid_type(type)) return fail(RD4_ETYPE, "KvType outside the enum%s");
+  if (width < 0 || (type >= RD4_KV_Q8_0 && width % 32 != 0))
+    return fail(RD4_EINVAL, "width must be a multiple of 32 for quantized types%s");
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & (type == RD4_KV_F32 ? 15 : type == RD4_KV_F16 ? 7 : 1)))
+    return fail(RD4_EINVAL, "src must be 16-byte aligned, dst aligned to its element store%s");
+  return launched(kv_store_launch(type, src, (uint8_t *)dst, width, (hipStream_t)stream),
+                  "kv store");
+}
+
+int rd4_kv_fill_launch(int type, void *cache, int64_t n_rows, int head_dim, uint32_t seed,
+                       void *stream) {
+  if (!valid_type(type)) return fail(RD4_ETYPE, "KvType outside the enum%s");
+  if (n_rows < 0 || head_dim <= 0 || head_dim % 32 != 0)
+    return fail(RD4_EINVAL, "head_dim must be a positive multiple of 32%s");
+  if ((uintptr_t)cache & (type == RD4_KV_F32 ? 15 : type == RD4_KV_F16 ? 7 : 1))
+    return fail(RD4_EINVAL, "cache pointer misaligned%s");
+  return launched(kv_fill_launch(type, (uint8_t *)cache, n_rows * head_dim, seed,
+                                 (hipStream_t)stream),
+                  "kv fill");
+}
+
+int rd4_kv_load_rows_launch(int type, const void *src, float *dst, int64_t width, void *stream) {
+  if (!valid_type(type)) return fail(RD4_ETYPE, "KvType outside the enum%s");
+  if (width < 0 || (type >= RD4_KV_Q8_0 && width % 32 != 0))
+    return fail(RD4_EINVAL, "width must be a multiple of 32 for quantized types%s");
+  if (((uintptr_t)dst & 15) || ((uintptr_t)src & 3))
+    return fail(RD4_EINVAL, "dst must be 16-byte and src 4-byte aligned%s");
+  return launched(kv_load_launch(type, (const uint8_t *)src, dst, width, (hipStream_t)stream),
+                  "kv load");
+}
+
+int rd4_attn_decode(const float *q, const void *k, const void *v, float *out, float *gate, int t,
+                    int n_head, int n_head_kv, int head_dim, float scale, int kt, int vt,
+                    int n_splits, void *stream) {
+  if (n_splits < 0) return fail(RD4_EINVAL, "n_splits must be >= 0%s");
+  int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
+  if (rc) return rc;
+  const int cps = n_head_kv * ((n_head / n_head_kv + 7) / 8);
+  const int s = n_splits ? n_splits : auto_splits(t + 1, cps);
+  return run_attn(q, k, v, out, gate, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt, vt,
+                  s, (hipStream_t)stream);
+}
+
+int rd4_attn_launch(const float *q, const void *k, const void *v, float *out, int t, int n_head,
+                    int n_head_kv, int head_dim, float scale, int kt, int vt, void *stream) {
+  return rd4_attn_decode(q, k, v, out, nullptr, t, n_head, n_head_kv, head_dim, scale, kt, vt, 0,
+                         stream);
+}
+
+int rd4_attn_launch_split(const float *q, const void *k, const void *v, float *out,
+                          float *partial, int t, int n_head, int n_head_kv, int head_dim,
+                          float scale, int kt, int vt, int n_splits, void *stream) {
+  (void)partial;
+  if (n_splits < 1) return fail(RD4_EINVAL, "n_splits must be >= 1%s");
+  int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
+  if (rc) return rc;
+  const int cps = n_head_kv * ((n_head / n_head_kv + 7) / 8);
+  int s = auto_splits(t + 1, cps);
+  if (s < n_splits) s = n_splits;
+  return run_attn(q, k, v, out, nullptr, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt,
+                  vt, s, (hipStream_t)stream);
+}
+
+int rd4_attn_launch_split_wpb(const float *q, const void *k, const void *v, float *out,
+                              float *partial, int t, int n_head, int n_head_kv, int head_dim,
+                              float scale, int kt, int vt, int n_splits, int wpb, void *stream) {
+  if (wpb != 8 && wpb != 16 && wpb != 32) return fail(RD4_EINVAL, "wpb must be 8, 16 or 32%s");
+  return rd4_attn_launch_split(q, k, v, out, partial, t, n_head, n_head_kv, head_dim, scale, kt,
+                               vt, n_splits, stream);
+}
+
+size_t rd4_attn_partial_bytes(int n_head, int head_dim, int n_splits) {
+  return (size_t)n_head * (size_t)n_splits * (2 + (size_t)head_dim) * sizeof(float);
+}
+
+int rd4_attn_split_wpb(int n_splits) { return (n_splits <= 4 || n_splits >= 16) ? 16 : 8; }
+
+int rd4_attn_batch_launch(const float *q, const void *k, const void *v, float *out,
+                          const int *pos, int n_tok, int n_head, int n_head_kv, int head_dim,
+                          float scale, int kt, int vt, void *stream) {
+  if (!pos) return fail(RD4_EINVAL, "pos must be a device array%s");
+  return run_attn(q, k, v, out, nullptr, pos, 0, n_tok, n_head, n_head_kv, head_dim, scale, kt,
+                  vt, 1, (hipStream_t)stream);
+}
+
+int rd4_attn_split_batch_launch(const float *q, const void *k, const void *v, float *out,
+                                float *partial, const int *pos, int n_tok, int n_head,
+                                int n_head_kv, int head_dim, float scale, int kt, int vt,
+                                int n_splits, void *stream) {
+  (void)partial;
+  if (!pos) return fail(RD4_EINVAL, "pos must be a device array%s");
+  if (n_splits < 1 || n_tok < 1) return fail(RD4_EINVAL, "n_splits and n_tok must be >= 1%s");
+  return run_attn(q, k, v, out, nullptr, pos, 0, n_tok, n_head, n_head_kv, head_dim, scale, kt,
+                  vt, n_splits, (hipStream_t)stream);
+}
+
+int rd4_fa2_prefill_usable(int kt, int vt, int n_q, int pos0, int n_head, int n_head_kv,
+                           int head_dim) {
+  const char *e = std::getenv("RD_GFX12_FA2_PREFILL");
+  if (e && std::atoi(e) == 0) return 0;
+  if (kt != RD4_KV_F16 || vt != RD4_KV_F16) return 0;
+  if (n_q < 1 || pos0 < 0) return 0;
+  return prefill_supported(kt, vt, n_head, n_head_kv, head_dim) ? 1 : 0;
+}
+
+int rd4_fa2_prefill_launch(const float *q, const void *k, const void *v, float *o,
+                           const int *pos, int n_q, int kmax, int keys_total, int n_head,
+                           int n_head_kv, int head_dim, float scale, void *stream) {
+  if (n_q < 1 || kmax < 0 || keys_total <= 0 || !pos)
+    return fail(RD4_EINVAL, "bad prefill shape%s");
+  int rc = check_attn_shape(n_head, n_head_kv, head_dim, RD4_KV_F16, RD4_KV_F16);
+  if (rc) return rc;
+  PrefillArgs p{};
+  p.q = q;
+  p.q_f16 = 0;
+  p.k = (const uint8_t *)k;
+  p.v = (const uint8_t *)v;
+  p.out = o;
+  p.gate = nullptr;
+  p.pos = pos;
+  p.pos0 = -1;
+  p.kmax = kmax < keys_total - 1 ? kmax : keys_total - 1;
+  p.n_q = n_q;
+  p.n_head = n_head;
+  p.n_head_kv = n_head_kv;
+  p.head_dim = head_dim;
+  p.scale = scale;
+  return launched(prefill_launch(RD4_KV_F16, RD4_KV_F16, p, (hipStream_t)stream), "prefill");
+}
+
+int rd4_prefill(const void *q, int q_f16, const void *k, const void *v, float *out, float *gate,
+                int pos0, int n_q, int n_head, int n_head_kv, int head_dim, float scale, int kt,
+                int vt, void *stream) {
+  if (n_q < 1 || pos0 < 0 || !q || !k || !v || !out) return fail(RD4_EINVAL, "bad prefill shape%s");
+  int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
+  if (rc) return rc;
+  PrefillArgs p{};
+  p.q = q;
+  p.q_f16 = q_f16 ? 1 : 0;
+  p.k = (const uint8_t *)k;
+  p.v = (const uint8_t *)v;
+  p.out = out;
+  p.gate = gate;
+  p.pos = nullptr;
+  p.pos0 = pos0;
+  p.kmax = pos0 + n_q - 1;
+  p.n_q = n_q;
+  p.n_head = n_head;
+  p.n_head_kv = n_head_kv;
+  p.head_dim = head_dim;
+  p.scale = scale;
+  return launched(prefill_launch(kt, vt, p, (hipStream_t)stream), "prefill");
+}
+
+int rd4_sigmoid_gate_launch(float *g_io, float *y_io, int64_t n, void *stream) {
+  if (n < 0 || (n > 0 && (!g_io || !y_io))) return fail(RD4_EINVAL, "bad gate buffers%s");
+  return launched(sigmoid_gate_launch(g_io, y_io, n, (hipStream_t)stream), "sigmoid gate");
+}
+
+int rd4_rope_launch(float *x, int n_tokens, int n_heads, int head_dim, int n_rot,
+                    float freq_base, const int *pos, void *stream) {
+  if (n_tokens < 0 || n_heads < 0 || n_rot < 0 || n_rot > head_dim || (n_rot & 1))
+    return fail(RD4_EINVAL, "bad rope shape%s");
+  return launched(
+      rope_launch(x, n_tokens, n_heads, head_dim, n_rot, freq_base, pos, (hipStream_t)stream),
+      "rope");
+}
+
+}  // extern "C"

@@ -1,0 +1,70 @@
+// Sigmoid output gate and split-half RoPE (gfx950).
+//
+// sigmoid_gate: nn.cuh:405-420 -- g <- 1/(1+exp(-g)); y <- y * g, element-wise.
+// rope: attn.cuh:30-63 -- pair (p, p + n_rot/2) of each head rotates by
+// pos[t] * freq_base^(-2p/n_rot). Both are element-local, so a thread takes 4
+// consecutive elements (gate) or one pair (rope).
+#include "common.hpp"
+
+namespace rd4 {
+
+__global__ __launch_bounds__(256) void sigmoid_gate_kernel(float *__restrict__ g,
+                                                           float *__restrict__ y, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= n) return;
+  if (i + 4 <= n && ((((uintptr_t)g) | ((uintptr_t)y)) & 15) == 0) {
+    float4 gv = *(float4 *)(g + i), yv = *(float4 *)(y + i);
+    gv.x = 1.0f / (1.0f + expf(-gv.x));
+    gv.y = 1.0f / (1.0f + expf(-gv.y));
+    gv.z = 1.0f / (1.0f + expf(-gv.z));
+    gv.w = 1.0f / (1.0f + expf(-gv.w));
+    yv.x *= gv.x;
+    yv.y *= gv.y;
+    yv.z *= gv.z;
+    yv.w *= gv.w;
+    *(float4 *)(g + i) = gv;
+    *(float4 *)(y + i) = yv;
+  } else {
+    for (int64_t k = i; k < n && k < i + 4; ++k) {
+      const float s = 1.0f / (1.0f + expf(-g[k]));
+      g[k] = s;
+      y[k] = y[k] * s;
+    }
+  }
+}
+
+__global__ __launch_bounds__(128) void rope_kernel(float *__restrict__ x, int n_tokens,
+                                                   int n_heads, int head_dim, int n_rot,
+                                                   float freq_base, const int *__restrict__ pos) {
+  const int pairs = n_rot / 2;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)n_tokens * n_heads * pairs) return;
+  const int p = (int)(idx % pairs);
+  const int64_t th = idx / pairs;  // token * n_heads + head
+  const int t = (int)(th / n_heads);
+  const float theta = (float)pos[t] * powf(freq_base, -2.0f * (float)p / (float)n_rot);
+  const float c = cosf(theta), s = sinf(theta);
+  float *b = x + th * head_dim;
+  const float x0 = b[p], x1 = b[p + pairs];
+  b[p] = x0 * c - x1 * s;
+  b[p + pairs] = x0 * s + x1 * c;
+}
+
+hipError_t sigmoid_gate_launch(float *g, float *y, int64_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const int64_t threads = (n + 3) / 4;
+  hipLaunchKernelGGL(sigmoid_gate_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     st, g, y, n);
+  return hipGetLastError();
+}
+
+hipError_t rope_launch(float *x, int n_tokens, int n_heads, int head_dim, int n_rot,
+                       float freq_base, const int *pos, hipStream_t st) {
+  const int64_t total = (int64_t)n_tokens * n_heads * (n_rot / 2);
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 127) / 128)), dim3(128), 0, st, x,
+                     n_tokens, n_heads, head_dim, n_rot, freq_base, pos);
+  return hipGetLastError();
+}
+
+}  // namespace rd4

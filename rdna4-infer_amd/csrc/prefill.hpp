@@ -1,0 +1,26 @@
+// Internal interface of the prefill and MFMA decode kernels.
+#pragma once
+#include "attn_generic.hpp"
+
+namespace rd4 {
+
+struct PrefillArgs {
+  const void *q;      // [n_q][n_head][hd], f32 or f16 (q_f16)
+  int q_f16;
+  const uint8_t *k, *v;
+  float *out;         // [n_q][n_head][hd] f32 (may alias q when q is f32)
+  float *gate;        // optional, same shape: logits in, sigmoid out
+  const int *pos;     // device positions, or nullptr -> pos0 + i
+  int pos0;
+  int kmax;           // last key index any query may attend
+  int n_q, n_head, n_head_kv, head_dim;
+  float scale;
+};
+
+bool prefill_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim);
+hipError_t prefill_launch(int kt, int vt, const PrefillArgs &p, hipStream_t st);
+
+bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim);
+hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a, int n_tok, hipStream_t st);
+
+}  // namespace rd4

@@ -1,0 +1,163 @@
+"""Decode / batched attention on the GPU vs the f64 CPU oracle (reference
+attn.cuh:95-1049 semantics; tolerance max-abs 2e-3, mean-rel 1e-3)."""
+import numpy as np
+import pytest
+
+from gpu_util import check_close, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def make_cache(orc, t, n, nkv, hd, seed, outlier=False):
+    x = orc.randn(n * nkv * hd, seed)
+    if outlier:
+        x = x.reshape(n, nkv, hd)
+        x[:, :, 7] *= 8
+        x = x.ravel()
+    return orc.store_rows(t, x)
+
+
+def run_decode(rd4, torch, dev, q, k, v, t, nh, nkv, hd, kt, vt, gate=None, n_splits=0):
+    out = torch.empty(nh * hd, dtype=torch.float32, device=dev)
+    g = None if gate is None else to_dev(gate, torch, dev)
+    rd4.attn_decode(to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev), out, t,
+                    nh, nkv, hd, 1.0 / np.sqrt(hd), kt, vt, gate=g, n_splits=n_splits)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().reshape(nh, hd), (None if g is None else g.cpu().numpy())
+
+
+def test_config1_cpu_reference_case(rd4, orc, dev):
+    """16 q heads / 2 kv heads, hd 256, f16 K/V x 512, no gate."""
+    import torch
+    nh, nkv, hd, n = 16, 2, 256, 512
+    k = make_cache(orc, 1, n, nkv, hd, 1)
+    v = make_cache(orc, 1, n, nkv, hd, 2)
+    q = orc.randn(nh * hd, 3)
+    want = orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, 1, 1)
+    got, _ = run_decode(rd4, torch, dev, q, k, v, n - 1, nh, nkv, hd, 1, 1)
+    check_close(got, want, "cfg1")
+
+
+PAIRS = [(kt, vt) for kt in range(6) for vt in range(6)]
+
+
+@pytest.mark.parametrize("kt,vt", PAIRS)
+def test_all_36_pairs(rd4, orc, dev, kt, vt):
+    """Every (K, V) storage pair dispatches (attn.cuh:203-246) and matches."""
+    import torch
+    nh, nkv, hd, n = 24, 4, 256, 300
+    k = make_cache(orc, kt, n, nkv, hd, 10 + kt)
+    v = make_cache(orc, vt, n, nkv, hd, 20 + vt)
+    q = orc.randn(nh * hd, 30)
+    want = orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, kt, vt)
+    got, _ = run_decode(rd4, torch, dev, q, k, v, n - 1, nh, nkv, hd, kt, vt, n_splits=3)
+    check_close(got, want, "pair %d/%d" % (kt, vt))
+
+
+@pytest.mark.parametrize("splits", [1, 2, 7, 16, 17, 64, 256])
+def test_split_invariance_and_merge_tree(rd4, orc, dev, splits):
+    """Any split count (one-level merge <= 16, two-level above) gives the same
+    attention, including splits with no keys (t+1 < splits*32)."""
+    import torch
+    nh, nkv, hd, n = 24, 4, 256, 1000
+    k = make_cache(orc, 2, n, nkv, hd, 40, outlier=True)
+    v = make_cache(orc, 2, n, nkv, hd, 41, outlier=True)
+    q = orc.randn(nh * hd, 42)
+    want = orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, 2, 2)
+    got, _ = run_decode(rd4, torch, dev, q, k, v, n - 1, nh, nkv, hd, 2, 2, n_splits=splits)
+    check_close(got, want, "splits %d" % splits)
+    # repeated launches reuse the self-resetting merge counters
+    got2, _ = run_decode(rd4, torch, dev, q, k, v, n - 1, nh, nkv, hd, 2, 2, n_splits=splits)
+    assert np.array_equal(got, got2)
+
+
+def test_more_splits_than_keys_and_no_keys(rd4, orc, dev):
+    import torch
+    nh, nkv, hd = 8, 2, 128
+    k = make_cache(orc, 1, 4, nkv, hd, 50)
+    v = make_cache(orc, 1, 4, nkv, hd, 51)
+    q = orc.randn(nh * hd, 52)
+    got, _ = run_decode(rd4, torch, dev, q, k, v, 0, nh, nkv, hd, 1, 1, n_splits=200)
+    want = np.tile(orc.load_rows(1, v, 4 * nkv * hd).reshape(4, nkv, hd)[0], (1, 4)).reshape(nkv, 4, hd)
+    check_close(got, np.repeat(orc.load_rows(1, v, 4 * nkv * hd).reshape(4, nkv, hd)[0], 4, 0), "1 key")
+    got, _ = run_decode(rd4, torch, dev, q, k, v, -1, nh, nkv, hd, 1, 1, n_splits=5)
+    assert np.all(got == 0)
+
+
+def test_gate_fused(rd4, orc, dev):
+    """rd4_attn_decode with a gate == attention then sigmoid_gate (graph.cuh:958-981)."""
+    import torch
+    nh, nkv, hd, n = 24, 4, 256, 2048
+    k = make_cache(orc, 2, n, nkv, hd, 60)
+    v = make_cache(orc, 2, n, nkv, hd, 61)
+    q = orc.randn(nh * hd, 62)
+    g = orc.randn(nh * hd, 63)
+    att = orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, 2, 2)
+    gs, want = orc.sigmoid_gate(g, att.ravel())
+    got, gg = run_decode(rd4, torch, dev, q, k, v, n - 1, nh, nkv, hd, 2, 2, gate=g)
+    check_close(got.ravel(), want, "gated")
+    assert np.allclose(gg, gs, rtol=1e-6, atol=1e-7)
+
+
+def test_reference_entry_points_in_place(rd4, orc, dev):
+    """attn_launch / attn_launch_split with q == out (graph.cuh:964-969)."""
+    import torch
+    nh, nkv, hd, n = 24, 4, 256, 700
+    k = make_cache(orc, 3, n, nkv, hd, 70)
+    v = make_cache(orc, 3, n, nkv, hd, 71)
+    q = orc.randn(nh * hd, 72)
+    want = orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, 3, 3)
+    kd, vd = to_dev(k, torch, dev), to_dev(v, torch, dev)
+    for fn in ("launch", "split"):
+        buf = to_dev(q, torch, dev)
+        if fn == "launch":
+            rd4.attn_launch(buf, kd, vd, buf, n - 1, nh, nkv, hd, 1 / 16, 3, 3)
+        else:
+            part = torch.empty(nh * 16 * (hd + 2), dtype=torch.float32, device=dev)
+            rd4.attn_launch_split(buf, kd, vd, buf, part, n - 1, nh, nkv, hd, 1 / 16, 3, 3, 4)
+        check_close(buf.cpu().numpy().reshape(nh, hd), want, fn)
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_batched(rd4, orc, dev, split):
+    """attn_batch_launch / attn_split_batch_launch: token i attends keys 0..pos[i]."""
+    import torch
+    nh, nkv, hd, n = 24, 4, 256, 1500
+    k = make_cache(orc, 2, n, nkv, hd, 80)
+    v = make_cache(orc, 1, n, nkv, hd, 81)
+    pos = np.int32([0, 1, 31, 32, 511, 512, 1200, 1499])
+    q = orc.randn(pos.size * nh * hd, 82).reshape(pos.size, nh, hd)
+    want = orc.attn_batch(q, k, v, pos, nh, nkv, hd, 1 / 16, 2, 1)
+    qd = to_dev(q, torch, dev)
+    out = torch.empty_like(qd)
+    args = (qd, to_dev(k, torch, dev), to_dev(v, torch, dev), out, to_dev(pos, torch, dev), nh, nkv,
+            hd, 1 / 16, 2, 1)
+    if split:
+        rd4.attn_split_batch(*args, 6)
+    else:
+        rd4.attn_batch(*args)
+    check_close(out.cpu().numpy(), want, "batch")
+
+
+def test_sigmoid_gate_kernel(rd4, orc, dev):
+    import torch
+    g = orc.randn(24 * 256 + 3, 90) * 4
+    y = orc.randn(g.size, 91)
+    gs, ys = orc.sigmoid_gate(g, y)
+    gd, yd = to_dev(g, torch, dev), to_dev(y, torch, dev)
+    rd4.sigmoid_gate(gd, yd)
+    assert np.allclose(gd.cpu().numpy(), gs, rtol=2e-6, atol=1e-7)
+    assert np.allclose(yd.cpu().numpy(), ys, rtol=3e-6, atol=1e-7)
+
+
+def test_rope_kernel(rd4, orc, dev):
+    import torch
+    nt, nh, hd, nrot = 5, 4, 256, 64
+    x = orc.randn(nt * nh * hd, 92).reshape(nt, nh, hd)
+    pos = np.int32([0, 1, 7, 4096, 131000])
+    want = orc.rope(x, nt, nh, hd, nrot, 1e7, pos)
+    xd = to_dev(x, torch, dev)
+    rd4.rope(xd, nt, nh, hd, nrot, 1e7, to_dev(pos, torch, dev))
+    got = xd.cpu().numpy()
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel < 1e-5  # f32 angle vs f64 oracle at positions up to 131000
