@@ -91,23 +91,21 @@ def decode_workload(torch, rd4, kt, ctx, outlier, gated=True):
     vrow = torch.randn(NKV * HD, generator=g, device="cuda")
     out = torch.empty(NH * HD, device="cuda")
     scale = 1.0 / np.sqrt(HD)
-    kslot = kc[pos * NKV * rb:(pos + 1) * NKV * rb]
-    vslot = vc[pos * NKV * rb:(pos + 1) * NKV * rb]
 
     def step(timer=None):
-        rd4.kv_store_rows(kt, krow, kslot)
-        rd4.kv_store_rows(kt, vrow, vslot)
+        # one launch: quantize-append the token's K/V rows at `pos`, gated attention over 0..pos
         if timer:
             timer.begin()
-        rd4.attn_decode(q, kc, vc, out, pos, NH, NKV, HD, scale, kt, kt, gate=gate if gated else None)
+        rd4.attn_decode_append(q, krow, vrow, kc, vc, out, pos, NH, NKV, HD, scale, kt, kt,
+                               gate=gate if gated else None)
         if timer:
             timer.end()
 
     kv_bytes = ctx * NKV * 2 * rb
     small = NH * HD * 4 * (4 if gated else 2)  # q, out (+ gate read and write)
     append = 2 * NKV * HD * 4 + 2 * NKV * rb
-    attn_bytes = kv_bytes + small
-    step_bytes = attn_bytes + append
+    attn_bytes = kv_bytes + small + append  # the append is inside the attention launch
+    step_bytes = attn_bytes
 
     def cpu(budget_s=12.0):
         """Scalar f64 oracle on the same cache, repeated for ~budget_s; returns GB/s."""

@@ -116,6 +116,15 @@ int rd4_attn_decode(const float *q, const void *k, const void *v, float *out, fl
                     int n_head, int n_head_kv, int head_dim, float scale, int kt, int vt,
                     int n_splits, void *stream);
 
+/* Native decode with the KV append fused in: quantizes k_new / v_new (f32
+ * [n_head_kv][head_dim], 16-byte aligned) into cache row t exactly like
+ * rd4_kv_store_row_launch, then attends keys 0..t -- the sequence
+ * kv_write_batch + attn_launch_split + sigmoid_gate_launch of graph.cuh:954-981
+ * in one launch. gate may be NULL. */
+int rd4_attn_decode_append(const float *q, const float *k_new, const float *v_new, void *k,
+                           void *v, float *out, float *gate, int t, int n_head, int n_head_kv,
+                           int head_dim, float scale, int kt, int vt, int n_splits, void *stream);
+
 /* ---- batched attention (attn.cuh:373-424, 958-1049) ---------------------- */
 
 /* attn_batch_launch (attn.cuh:373): token i of n_tok attends keys 0..pos[i]

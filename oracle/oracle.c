@@ -444,7 +444,9 @@ void orc_rope(float *x, int n_tokens, int n_heads, int head_dim, int n_rot, floa
     for (int h = 0; h < n_heads; ++h) {
       float *b = x + ((int64_t)t * n_heads + h) * head_dim;
       for (int p = 0; p < pairs; ++p) {
-        const double th = (double)pos[t] * pow((double)freq_base, -2.0 * p / (double)n_rot);
+        /* the angle is formed in f32 like attn.cuh:39; cos/sin then in double */
+        const float thf = (float)pos[t] * powf(freq_base, -2.0f * (float)p / (float)n_rot);
+        const double th = (double)thf;
         const double c = cos(th), s = sin(th);
         const double x0 = b[p], x1 = b[p + pairs];
         b[p] = (float)(x0 * c - x1 * s);

@@ -60,7 +60,7 @@ void orc_merge(const float *partial, float *out, int n_rows, int head_dim, int n
 /* g <- sigmoid(g); y <- y * g, f32 (nn.cuh:110,405-412). */
 void orc_sigmoid_gate(float *g, float *y, int64_t n);
 
-/* Split-half RoPE over the first n_rot dims (attn.cuh:30-54), in double. */
+/* Split-half RoPE over the first n_rot dims (attn.cuh:30-54): f32 angle, double rotation. */
 void orc_rope(float *x, int n_tokens, int n_heads, int head_dim, int n_rot, float freq_base,
               const int *pos);
 

@@ -35,6 +35,7 @@ SIGNATURES = {
     "rd4_attn_partial_bytes": ([_I, _I, _I], ctypes.c_size_t),
     "rd4_attn_split_wpb": ([_I], _I),
     "rd4_attn_decode": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
+    "rd4_attn_decode_append": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
     "rd4_attn_batch_launch": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P], _I),
     "rd4_attn_split_batch_launch": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
     "rd4_fa2_prefill_launch": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
@@ -135,6 +136,14 @@ def attn_decode(q, k, v, out, t, n_head, n_head_kv, head_dim, scale, kt, vt, gat
     _check(lib().rd4_attn_decode(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(gate), t, n_head,
                                  n_head_kv, head_dim, scale, kt, vt, n_splits, _stream()),
            "attn_decode")
+
+
+def attn_decode_append(q, k_new, v_new, k, v, out, t, n_head, n_head_kv, head_dim, scale, kt, vt,
+                       gate=None, n_splits=0):
+    """Append the token's K/V rows at position t, then gated decode over keys 0..t."""
+    _check(lib().rd4_attn_decode_append(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k), _ptr(v), _ptr(out),
+                                        _ptr(gate), t, n_head, n_head_kv, head_dim, scale, kt, vt,
+                                        n_splits, _stream()), "attn_decode_append")
 
 
 def attn_launch(q, k, v, out, t, n_head, n_head_kv, head_dim, scale, kt, vt):

@@ -17,6 +17,7 @@
 //
 // This kernel is the all-types path; the MFMA kernels in attn_decode_mfma.hip
 // take the hot (K, V) pairs.
+#include "kv_quant.hpp"
 #include "merge.hpp"
 
 namespace rd4 {
@@ -83,6 +84,27 @@ __global__ __launch_bounds__(kThreads) void attn_generic_kernel(AttnArgs a) {
   uint8_t *k_t = (uint8_t *)(flag + 4);                        // [kTK][kls]
   uint8_t *v_t = k_t + kTK * kls;                              // [kTK][vls]
 
+  const int64_t kstride = (int64_t)a.n_head_kv * krb, vstride = (int64_t)a.n_head_kv * vrb;
+  const uint8_t *kbase = a.k + (int64_t)kvh * krb;
+  const uint8_t *vbase = a.v + (int64_t)kvh * vrb;
+
+  // Fused append: the CTA owning key t first writes the new K/V row of its kv head.
+  if (a.k_new && j_begin <= t && t < j_end) {
+    const bool isv = tid >= 128;
+    const int u = tid & 127;
+    if (u < hd / 4) {
+      const float *src = (isv ? a.v_new : a.k_new) + (int64_t)kvh * hd + 4 * u;
+      float x[4] = {src[0], src[1], src[2], src[3]};
+      uint8_t *row = (uint8_t *)(isv ? vbase : kbase) + (int64_t)t * (isv ? vstride : kstride);
+      if (isv)
+        store_group4<VT>(x, tid & 7, row, u >> 3);
+      else
+        store_group4<KT>(x, tid & 7, row, u >> 3);
+    }
+  }
+  if (a.k_new) __threadfence();
+  __syncthreads();
+
   const int64_t qoff = ((int64_t)tok * a.n_head + h0) * hd;
   if (a.q_f16) {
     const uint16_t *qh = (const uint16_t *)a.q;
@@ -110,10 +132,6 @@ __global__ __launch_bounds__(kThreads) void attn_generic_kernel(AttnArgs a) {
   // QK ownership: key lane kj, dim slice sl of hd/8 dims.
   const int kj = tid & (kTK - 1), sl = tid / kTK;
   const int sl_len = hd >> 3;
-
-  const int64_t kstride = (int64_t)a.n_head_kv * krb, vstride = (int64_t)a.n_head_kv * vrb;
-  const uint8_t *kbase = a.k + (int64_t)kvh * krb;
-  const uint8_t *vbase = a.v + (int64_t)kvh * vrb;
 
   for (int j0 = j_begin; j0 < j_end; j0 += kTK) {
     const int nk = min(kTK, j_end - j0);

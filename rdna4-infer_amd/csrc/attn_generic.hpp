@@ -14,6 +14,8 @@ struct AttnArgs {
   const uint8_t *v;
   float *out;             // [n_tok][n_head][hd] f32 (may alias q)
   float *gate;            // optional [n_tok][n_head][hd]: in logits, out sigmoid
+  const float *k_new;     // optional fused append (single token): f32 [n_head_kv][hd] rows
+  const float *v_new;     //   written to cache row t before it is attended
   const int *pos;         // device positions per token, or nullptr -> t
   int t;                  // last key index for the single-token launch
   int n_head, n_head_kv, head_dim;

@@ -96,7 +96,8 @@ int auto_splits(int keys, int ctas_per_split) {
 // Common body of every decode-style launch.
 int run_attn(const float *q, const void *k, const void *v, float *out, float *gate,
              const int *pos, int t, int n_tok, int n_head, int n_head_kv, int head_dim,
-             float scale, int kt, int vt, int splits, hipStream_t st) {
+             float scale, int kt, int vt, int splits, hipStream_t st,
+             const float *k_new = nullptr, const float *v_new = nullptr) {
   int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
   if (rc) return rc;
   if (n_tok < 1) return fail(RD4_EINVAL, "n_tok must be >= 1%s");
@@ -111,6 +112,8 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   a.v = (const uint8_t *)v;
   a.out = out;
   a.gate = gate;
+  a.k_new = k_new;
+  a.v_new = v_new;
   a.pos = pos;
   a.t = t;
   a.n_head = n_head;
@@ -133,7 +136,8 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
     a.l1_offset = (int64_t)n_tok * n_head * splits * rec;
   }
   a.n_splits = splits;
-  if (decode_mfma_supported(kt, vt, n_head, n_head_kv, head_dim))
+  const bool aligned16 = ((((uintptr_t)k) | ((uintptr_t)v)) & 15) == 0;
+  if (aligned16 && decode_mfma_supported(kt, vt, n_head, n_head_kv, head_dim))
     return launched(decode_mfma_launch(kt, vt, a, n_tok, st), "decode kernel");
   return launched(attn_generic_launch(kt, vt, a, n_tok, st), "attention kernel");
 }
@@ -217,6 +221,23 @@ int rd4_attn_decode(const float *q, const void *k, const void *v, float *out, fl
   const int s = n_splits ? n_splits : auto_splits(t + 1, cps);
   return run_attn(q, k, v, out, gate, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt, vt,
                   s, (hipStream_t)stream);
+}
+
+int rd4_attn_decode_append(const float *q, const float *k_new, const float *v_new, void *k,
+                           void *v, float *out, float *gate, int t, int n_head, int n_head_kv,
+                           int head_dim, float scale, int kt, int vt, int n_splits, void *stream) {
+  if (n_splits < 0 || t < 0 || !k_new || !v_new)
+    return fail(RD4_EINVAL, "append needs t >= 0, n_splits >= 0 and both new rows%s");
+  if ((((uintptr_t)k_new) | ((uintptr_t)v_new)) & 15)
+    return fail(RD4_EINVAL, "new rows must be 16-byte aligned%s");
+  int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
+  if (rc) return rc;
+  if ((kt >= RD4_KV_Q8_0 && ((uintptr_t)k & 1)) || (vt >= RD4_KV_Q8_0 && ((uintptr_t)v & 1)))
+    return fail(RD4_EINVAL, "cache pointers misaligned%s");
+  const int cps = n_head_kv * ((n_head / n_head_kv + 7) / 8);
+  const int s = n_splits ? n_splits : auto_splits(t + 1, cps);
+  return run_attn(q, k, v, out, gate, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt, vt,
+                  s, (hipStream_t)stream, k_new, v_new);
 }
 
 int rd4_attn_launch(const float *q, const void *k, const void *v, float *out, int t, int n_head,

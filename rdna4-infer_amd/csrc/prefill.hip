@@ -27,9 +27,4 @@ hipError_t prefill_launch(int kt, int vt, const PrefillArgs &p, hipStream_t st) 
   return attn_generic_launch(kt, vt, a, p.n_q, st);
 }
 
-bool decode_mfma_supported(int, int, int, int, int) { return false; }
-hipError_t decode_mfma_launch(int, int, const AttnArgs &, int, hipStream_t) {
-  return hipErrorInvalidValue;
-}
-
 }  // namespace rd4
