@@ -10,7 +10,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librdna4attn.so")
+LIB_PATH = os.environ.get("RD4_LIB") or os.path.join(HERE, "librdna4attn.so")
 
 F32, F16, Q8_0, Q4_0, Q5_0, Q4_1 = range(6)
 TYPE_NAMES = ("f32", "f16", "q8_0", "q4_0", "q5_0", "q4_1")

@@ -28,7 +28,18 @@ def _compile(src):
     return src, r.returncode, obj, "\n".join(msgs)
 
 
-def build(verbose=True):
+def build(verbose=True, out=None, extra=()):
+    """Compile every source and link the library (to `out`, default in-tree)."""
+    global FLAGS
+    flags0 = FLAGS
+    FLAGS = FLAGS + list(extra)
+    try:
+        return _build(verbose, out or LIB)
+    finally:
+        FLAGS = flags0
+
+
+def _build(verbose, lib_path):
     os.makedirs(OBJ, exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
         results = list(ex.map(_compile, SOURCES))
@@ -38,10 +49,13 @@ def build(verbose=True):
             print("[%s]\n%s" % (src, msg), file=sys.stderr)
     if bad:
         raise RuntimeError("hipcc failed for: " + ", ".join(b[0] for b in bad))
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB] + [r[2] for r in results]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", lib_path] + [r[2] for r in results]
     subprocess.run(cmd, check=True)
-    return LIB
+    return lib_path
 
 
 if __name__ == "__main__":
-    print(build())
+    # python build.py [out.so] [-DNAME=VALUE ...]: variant builds for experiments
+    args = sys.argv[1:]
+    out = next((a for a in args if a.endswith(".so")), None)
+    print(build(out=out, extra=[a for a in args if a.startswith("-D")]))

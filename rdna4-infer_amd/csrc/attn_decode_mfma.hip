@@ -5,10 +5,10 @@
 // nn.cuh:405-412 and the append of graph.cuh:1011-1031 optionally fused:
 // out[h] = softmax_j(q_h . k_j * scale) . V over keys 0..t, f32 accumulation.
 //
-// Work decomposition: CTA = 4 waves = one (token, kv head, <=8-query-head
-// chunk, key split). Each wave walks its own 32-key tiles of the split
-// (tiles w, w+4, ...) with a private online-softmax state, so the main loop
-// has no CTA barrier. Per tile:
+// Work decomposition: CTA = 8 waves = one (token, kv head, <=8-query-head
+// chunk, key split). Each wave walks its own 16-key tiles of the split
+// (tiles w, w+8, ...: the 8 waves stream adjacent memory) with a private
+// online-softmax state, so the main loop has no CTA barrier. Per tile:
 //   1. the tile's raw K and V rows (exactly the cache bytes) arrive with
 //      16-byte global loads issued one tile ahead into registers, and are
 //      written to a wave-private LDS buffer;
@@ -19,10 +19,11 @@
 //      costs no precision. Quantized K is scaled by its per-(key, block) d after
 //      each 32-dim block's MFMA;
 //   3. online softmax in registers (exp2 domain); the C layout of S^T gives each
-//      lane one query row x 8 keys, exactly the B operand layout PV needs;
-//   4. O^T += V^T P^T on the same MFMA: A = 16 dims x 32 keys of V read from
-//      LDS, B = p (hi/lo rows again), with the quantized V's d folded into p per
-//      32-dim block.
+//      lane one query row x 4 keys, exactly the B operand layout PV needs; the
+//      O rescale is skipped when no row's running max moved;
+//   4. O^T += V^T P^T on v_mfma_f32_16x16x16_f16: A = 16 dims x 16 keys of V
+//      read from LDS, B = p (hi/lo rows again), with the quantized V's d folded
+//      into p per 32-dim block.
 // The 4 waves' states merge through LDS into one (m, l, acc) record per query
 // head; splits merge through the two-level tree of merge.hpp in the same launch.
 #include <cstdlib>
@@ -40,44 +41,60 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kHD = 256;     // head_dim of this kernel
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kTile = 32;    // keys per wave tile
+constexpr int kTile = 16;    // keys per wave tile
 constexpr int kG = 8;        // query heads per CTA (MFMA rows 0-7 hi, 8-15 lo)
 constexpr float kLog2e = 1.4426950408889634f;
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+// Wait until at most N of this wave's vector memory loads are outstanding
+// (loads complete in issue order); also a compiler memory barrier.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 template <int T>
 __host__ __device__ constexpr int rowb() {
   return T == F16 ? kHD * 2 : (kHD / 32) * block_bytes(T);
 }
-// LDS row stride: 16-byte multiple whose word count is not a multiple of 64,
-// so 16 lanes reading one column of 16 rows do not share a bank.
-template <int T>
-__host__ __device__ constexpr int lds_stride() {
-  return (rowb<T>() / 4) % 64 == 0 ? rowb<T>() + 16 : rowb<T>();
-}
 template <int T>
 __host__ __device__ constexpr int chunks_per_row() {
   return rowb<T>() / 16;
 }
-template <int KT, int VT>
-__host__ __device__ constexpr int tile_chunks() {
-  return kTile * (chunks_per_row<KT>() + chunks_per_row<VT>());
+// f16 rows are 32 chunks (512 B, a multiple of the 64 banks): the chunk of
+// global column c in row r sits at slot c ^ (r & 15) so 16 lanes reading one
+// column of 16 rows hit 16 different banks. Block-quantized rows (17 or 9
+// chunks) are conflict-free unswizzled.
+template <int T>
+__device__ __forceinline__ int swz(int row, int col) {
+  return T == F16 ? (col ^ (row & 15)) : col;
 }
+
+// Tile image in LDS: the tile's K rows then V rows, contiguous 16-byte chunks,
+// padded to whole 64-chunk load instructions.
 template <int KT, int VT>
-__host__ __device__ constexpr int regs_per_lane() {
-  return (tile_chunks<KT, VT>() + 63) / 64;
-}
-template <int KT, int VT>
-__host__ __device__ constexpr int wave_lds_bytes() {
-  return kTile * (lds_stride<KT>() + lds_stride<VT>());
-}
+struct TileShape {
+  static constexpr int KC = chunks_per_row<KT>(), VC = chunks_per_row<VT>();
+  static constexpr int KCH = kTile * KC, VCH = kTile * VC;
+  static constexpr int NI = (KCH + VCH + 63) / 64;  // load instructions per tile
+  static constexpr int TB = NI * 1024;              // bytes per ring stage
+  // per-wave f32 scale tables [block][key] for the quantized K and V of a tile
+  static constexpr int DT = (KT != F16 ? 512 : 0) + (VT != F16 ? 512 : 0);
+#ifndef RD4_DEC_WAVES_SMALL
+#define RD4_DEC_WAVES_SMALL 8
+#endif
+#ifndef RD4_DEC_RMAX
+#define RD4_DEC_RMAX 3
+#endif
+  static constexpr int WAVES = TB <= 10240 ? RD4_DEC_WAVES_SMALL : 4;
+  static constexpr int R0 = (152 * 1024 / WAVES - DT) / TB;
+  static constexpr int R = R0 < 2 ? 2 : (R0 > RD4_DEC_RMAX ? RD4_DEC_RMAX : R0);  // ring stages per wave
+};
 
 __device__ __forceinline__ uint32_t lds_u16(const uint8_t *p) { return *(const uint16_t *)p; }
 __device__ __forceinline__ uint32_t lds_u8(const uint8_t *p) { return *p; }
@@ -105,10 +122,10 @@ __device__ __forceinline__ uint32_t nib2_to_h2(uint32_t v) {
 // A operand of S^T = K Q^T for one 16-key half and one 32-dim block: lane
 // (key = l%16, g = l/16) gets dims 32b + 8g .. +7 of its key, as f16.
 template <int KT>
-__device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g) {
+__device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g, int n_of_row) {
   u32x4 r;
   if constexpr (KT == F16) {
-    r = *(const u32x4 *)(krow + 2 * (32 * b + 8 * g));
+    r = *(const u32x4 *)(krow + 16 * ((4 * b + g) ^ n_of_row));
   } else if constexpr (KT == Q8_0) {
     const uint8_t *p = krow + 34 * b + 2 + 8 * g;
 #pragma unroll
@@ -125,47 +142,47 @@ __device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g) {
   return __builtin_bit_cast(half8, r);
 }
 
-// A operand of O^T = V^T P^T for dim d (this lane's) and the 8 keys of k-slots
-// 8g..8g+7 (keys 4g..4g+3 and 16+4g..16+4g+3 of the tile), as f16.
+// A operand of O^T = V^T P^T (v_mfma_f32_16x16x16_f16) for dim d (this lane's)
+// and keys 4g..4g+3 of the tile, as f16.
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 template <int VT>
-__device__ __forceinline__ half8 v_frag(const uint8_t *vt, int d, int g) {
-  constexpr int vs = lds_stride<VT>();
-  uint32_t e[8];
+__device__ __forceinline__ half4 v_frag(const uint8_t *vt, int d, int g) {
+  constexpr int vs = rowb<VT>();
+  const uint8_t *p0 = vt + 4 * g * vs;
+  uint32_t e[4];
+  uint32_t r0, r1;
   if constexpr (VT == F16) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = (i < 4) ? 4 * g + i : 16 + 4 * g + i - 4;
-      e[i] = lds_u16(vt + key * vs + 2 * d);
-    }
-    u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = e[2 * i] | (e[2 * i + 1] << 16);
-    return __builtin_bit_cast(half8, r);
+    for (int i = 0; i < 4; ++i)
+      e[i] = lds_u16(p0 + i * vs + 16 * ((d >> 3) ^ ((4 * g + i) & 15)) + 2 * (d & 7));
+    r0 = e[0] | (e[1] << 16);
+    r1 = e[2] | (e[3] << 16);
   } else if constexpr (VT == Q8_0) {
+    // bytes land in the low byte of 16-bit halves; 0x64 | b^0x80 per half is
+    // the f16 1024 + b + 128, so one xor and one packed add give b exactly
     const int off = 34 * (d >> 5) + 2 + (d & 31);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = (i < 4) ? 4 * g + i : 16 + 4 * g + i - 4;
-      e[i] = lds_u8(vt + key * vs + off);
-    }
-    u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = i8x2_to_h2(e[2 * i] | (e[2 * i + 1] << 8));
-    return __builtin_bit_cast(half8, r);
+    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 a0, a1;
+    a0.x = p0[off];
+    a0.y = p0[vs + off];
+    a1.x = p0[2 * vs + off];
+    a1.y = p0[3 * vs + off];
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    r0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_bit_cast(uint32_t, a0) ^ 0x64806480u) + c);
+    r1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_bit_cast(uint32_t, a1) ^ 0x64806480u) + c);
+    (void)e;
   } else {
     const int j = d & 31;
     const int off = 18 * (d >> 5) + 2 + (j & 15);
     const int sh = (j & 16) ? 4 : 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = (i < 4) ? 4 * g + i : 16 + 4 * g + i - 4;
-      e[i] = (lds_u8(vt + key * vs + off) >> sh) & 0xfu;
-    }
-    u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = nib2_to_h2(e[2 * i] | (e[2 * i + 1] << 16));
-    return __builtin_bit_cast(half8, r);
+    for (int i = 0; i < 4; ++i) e[i] = (lds_u8(p0 + i * vs + off) >> sh) & 0xfu;
+    r0 = nib2_to_h2(e[0] | (e[1] << 16));
+    r1 = nib2_to_h2(e[2] | (e[3] << 16));
   }
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(half4, u32x2{r0, r1});
 }
 
 template <int T>
@@ -180,12 +197,13 @@ __device__ __forceinline__ _Float16 lo_part(float x) { return (_Float16)(x - (fl
 }  // namespace
 
 template <int KT, int VT>
-__global__ __launch_bounds__(kThreads, (KT == F16 || VT == F16) ? 1 : 2) void decode_mfma_kernel(AttnArgs a) {
+__global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfma_kernel(AttnArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
-  constexpr int WL = wave_lds_bytes<KT, VT>();
-  constexpr int KS = lds_stride<KT>(), VS = lds_stride<VT>();
-  constexpr int KC = chunks_per_row<KT>(), VC = chunks_per_row<VT>();
-  constexpr int NR = regs_per_lane<KT, VT>();
+  using TS = TileShape<KT, VT>;
+  constexpr int kWaves = TS::WAVES, kThreads = 64 * kWaves;
+  constexpr int KS = rowb<KT>(), VS = rowb<VT>();
+  constexpr int KC = TS::KC, VC = TS::VC, KCH = TS::KCH, VCH = TS::VCH, NI = TS::NI;
+  constexpr int TB = TS::TB, R = TS::R, DT = TS::DT;
 
   const int s = blockIdx.x;
   const int kvh = blockIdx.y / a.n_chunks;
@@ -209,169 +227,208 @@ __global__ __launch_bounds__(kThreads, (KT == F16 || VT == F16) ? 1 : 2) void de
   const uint8_t *kbase = a.k + (int64_t)kvh * rowb<KT>();
   const uint8_t *vbase = a.v + (int64_t)kvh * rowb<VT>();
 
-  // Fused append: the CTA owning key t writes the new K/V row of its kv head.
-  if (a.k_new && j_begin <= t && t < j_end) {
-    const int sub = tid & 7;
-    const bool isv = tid >= 128;
-    const int u = tid & 127;  // 8 blocks x 8 lanes per row side (hd 256 -> 64 lanes used)
-    if (u < kHD / 4) {
-      const float *src = (isv ? a.v_new : a.k_new) + (int64_t)kvh * kHD + 4 * u;
-      float x[4] = {src[0], src[1], src[2], src[3]};
-      uint8_t *row = (uint8_t *)(isv ? vbase : kbase) + (int64_t)t * (isv ? vstride : kstride);
-      if (isv)
-        store_group4<VT>(x, sub, row, u >> 3);
-      else
-        store_group4<KT>(x, sub, row, u >> 3);
-    }
+  // Fused append: the CTA owning key t writes the new K/V row of its kv head
+  // (8-lane groups per 32-element block, the store kernel's quantizer).
+  if (a.k_new && j_begin <= t && t < j_end && tid < 128) {
+    const bool isv = tid >= 64;
+    const int u = tid & 63;
+    const float *src = (isv ? a.v_new : a.k_new) + (int64_t)kvh * kHD + 4 * u;
+    float x[4] = {src[0], src[1], src[2], src[3]};
+    uint8_t *row = (uint8_t *)(isv ? vbase : kbase) + (int64_t)t * (isv ? vstride : kstride);
+    if (isv)
+      store_group4<VT>(x, u & 7, row, u >> 3);
+    else
+      store_group4<KT>(x, u & 7, row, u >> 3);
   }
-  if (a.k_new) __threadfence();  // the new row is visible before any wave loads it
+  // the new row reaches this CU's L1 before any wave loads it (workgroup scope only)
+  if (a.k_new) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   __syncthreads();
 
   // Query fragment (B operand of S^T = K Q^T): row n is head n (hi) or n-8 (lo).
+  // All of this lane's query loads are issued before any is used.
   half8 qf[8];
   {
     const int hh = n & 7;
     const bool on = hh < G;
-    const int64_t qoff = (((int64_t)tok * a.n_head + h0 + hh) * kHD);
+    const int64_t qoff = (((int64_t)tok * a.n_head + h0 + (on ? hh : 0)) * kHD) + 8 * g;
+    float qv[8][8];
+    if (a.q_f16) {
+      u32x4 r[8];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+      for (int b = 0; b < 8; ++b) r[b] = *(const u32x4 *)((const uint16_t *)a.q + qoff + 32 * b);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int d = 32 * b + 8 * g + i;
-        float qv = 0.0f;
-        if (on) qv = a.q_f16 ? h2f(((const uint16_t *)a.q)[qoff + d]) : a.q[qoff + d];
-        qf[b][i] = (n < 8) ? hi_part(qv) : lo_part(qv);
+      for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          qv[b][2 * i] = h2f((uint16_t)r[b][i]);
+          qv[b][2 * i + 1] = h2f((uint16_t)(r[b][i] >> 16));
+        }
+    } else {
+      float4 r[16];
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        r[2 * b] = *(const float4 *)(a.q + qoff + 32 * b);
+        r[2 * b + 1] = *(const float4 *)(a.q + qoff + 32 * b + 4);
+      }
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        qv[b][0] = r[2 * b].x; qv[b][1] = r[2 * b].y; qv[b][2] = r[2 * b].z; qv[b][3] = r[2 * b].w;
+        qv[b][4] = r[2 * b + 1].x; qv[b][5] = r[2 * b + 1].y; qv[b][6] = r[2 * b + 1].z; qv[b][7] = r[2 * b + 1].w;
       }
     }
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        qf[b][i] = on ? ((n < 8) ? hi_part(qv[b][i]) : lo_part(qv[b][i])) : (_Float16)0.0f;
   }
   const float sl2 = a.scale * kLog2e;
-
-  uint8_t *wl = smem + w * WL;  // this wave's LDS: K rows then V rows
-  uint8_t *kl = wl, *vl = wl + kTile * KS;
 
   floatx4 o[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  const int n_tiles = (j_end - j_begin + kTile - 1) / kTile;
-  u32x4 raw[NR];
-
-  auto issue = [&](int tile) {
-    const int j0 = j_begin + tile * kTile;
-    const int nk = min(kTile, j_end - j0);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const int c = lane + 64 * r;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (c < kTile * KC) {
-        const int row = c / KC, col = c - row * KC;
-        if (row < nk) v = *(const u32x4 *)(kbase + (int64_t)(j0 + row) * kstride + 16 * col);
-      } else if (c < tile_chunks<KT, VT>()) {
-        const int cc = c - kTile * KC;
-        const int row = cc / VC, col = cc - row * VC;
-        if (row < nk) v = *(const u32x4 *)(vbase + (int64_t)(j0 + row) * vstride + 16 * col);
-      }
-      raw[r] = v;
+  // ---- async tile ring: stage i of this wave at ring + (i % R) * TB
+  uint8_t *ring = smem + w * (R * TB + DT);
+  float *dk_t = (float *)(ring + R * TB);                  // [8][16] K scales (quantized K)
+  float *dv_t = dk_t + (KT != F16 ? 128 : 0);              // [8][16] V scales (quantized V)
+  const int n_tiles_all = (j_end - j_begin + kTile - 1) / kTile;
+  const int my_tiles = (a.dbg & 32) ? 0 : (n_tiles_all > w ? (n_tiles_all - w + kWaves - 1) / kWaves : 0);
+  // Global source of this lane's chunk in load instruction r of a full tile:
+  // byte offset from the tile's K (or V) base, with the f16 swizzle applied.
+  auto src_of = [&](int r, int nk, const uint8_t *kt0, const uint8_t *vt0) -> const uint8_t * {
+    const int c = lane + 64 * r;
+    if (c < KCH) {
+      const int row = c / KC, slot = c - row * KC;
+      const int col = swz<KT>(row, slot);
+      return kt0 + (row < nk ? row * (int)kstride + 16 * col : 16 * col);
     }
+    const int cv = c < KCH + VCH ? c - KCH : 0;
+    const int row = cv / VC, slot = cv - row * VC;
+    const int col = swz<VT>(row, slot);
+    return vt0 + (row < nk ? row * (int)vstride + 16 * col : 16 * col);
   };
-  auto stash = [&]() {
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const int c = lane + 64 * r;
-      if (c < kTile * KC) {
-        const int row = c / KC, col = c - row * KC;
-        *(u32x4 *)(kl + row * KS + 16 * col) = raw[r];
-      } else if (c < tile_chunks<KT, VT>()) {
-        const int cc = c - kTile * KC;
-        const int row = cc / VC, col = cc - row * VC;
-        *(u32x4 *)(vl + row * VS + 16 * col) = raw[r];
-      }
-    }
-  };
-
-  int tile = w;
-  if (tile < n_tiles) issue(tile);
-  for (; tile < n_tiles; tile += kWaves) {
-    const int j0 = j_begin + tile * kTile;
+  auto issue = [&](int i) {  // i-th tile of this wave
+    const int j0 = j_begin + (w + i * kWaves) * kTile;
     const int nk = min(kTile, j_end - j0);
-    wave_sync();  // previous tile's LDS reads are done
-    stash();
+    const uint8_t *kt0 = kbase + (int64_t)j0 * kstride;
+    const uint8_t *vt0 = vbase + (int64_t)j0 * vstride;
+    uint8_t *st = ring + (i % R) * TB;
+#pragma unroll
+    for (int r = 0; r < NI; ++r)
+      __builtin_amdgcn_global_load_lds((const void *)src_of(r, nk, kt0, vt0),
+                                       (lds_void *)(st + 1024 * r), 16, 0, 0);
+  };
+#pragma unroll
+  for (int i = 0; i < R - 1; ++i)
+    if (i < my_tiles) issue(i);
+
+  for (int i = 0; i < my_tiles; ++i) {
+    const int nk = min(kTile, j_end - (j_begin + (w + i * kWaves) * kTile));
+    if (i + R - 1 < my_tiles) {
+      // the stage being refilled was read by the previous iteration: those reads are done
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue(i + R - 1);
+    }
+    // tile i is complete once at most the loads of the tiles issued after it remain
+    const int after = min(R - 1, my_tiles - 1 - i);
+    if (after >= 3) wait_vm<3 * NI>();
+    else if (after == 2) wait_vm<2 * NI>();
+    else if (after == 1) wait_vm<NI>();
+    else wait_vm<0>();
     wave_sync();
-    if (tile + kWaves < n_tiles) issue(tile + kWaves);
-
-    // ---- S^T = K Q^T for the two 16-key halves
-    float sc[8];
+    const uint8_t *kl = ring + (i % R) * TB;
+    const uint8_t *vl = kl + KCH * 16;
+    if constexpr (DT > 0) {  // f16 scales of the tile -> f32 tables, once per tile
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint8_t *krow = kl + (16 * h + n) * KS;
-      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < DT / 256; ++j) {
+        const int v = lane + 64 * j;
+        const bool isv = (KT == F16) || (VT != F16 && v >= 128);
+        const int vv = v & 127, key = vv & 15, b = vv >> 4;
+        const float d = isv ? scale_of<VT>(vl + key * VS, b) : scale_of<KT>(kl + key * KS, b);
+        (isv ? dv_t : dk_t)[b * 16 + key] = d;
+      }
+      wave_sync();
+    }
+
+    // ---- S^T = K Q^T: lane holds keys 4g..4g+3 of row n
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (a.dbg & 2) {
+      acc = floatx4{(float)lane, 1.f, 2.f, 3.f};
+    } else {
+      const uint8_t *krow = kl + n * KS;
       if constexpr (KT == F16) {
 #pragma unroll
         for (int b = 0; b < 8; ++b)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g), qf[b], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n), qf[b], acc, 0, 0, 0);
       } else {
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
           const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-          const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g), qf[b], z, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float d = scale_of<KT>(kl + (16 * h + 4 * g + i) * KS, b);
-            acc[i] = fmaf(d, c[i], acc[i]);
-          }
+          const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n), qf[b], z, 0, 0, 0);
+          const float4 dk = *(const float4 *)(dk_t + b * 16 + 4 * g);
+          acc[0] = fmaf(dk.x, c[0], acc[0]);
+          acc[1] = fmaf(dk.y, c[1], acc[1]);
+          acc[2] = fmaf(dk.z, c[2], acc[2]);
+          acc[3] = fmaf(dk.w, c[3], acc[3]);
         }
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc[4 * h + i] = acc[i];
     }
     // rows n and n^8 are the hi and lo halves of the same head
+    float sc[4];
     float tmax = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = (i < 4) ? 4 * g + i : 16 + 4 * g + i - 4;
-      float v = (sc[i] + xor_f(sc[i], 8)) * sl2;
-      if (key >= nk) v = -INFINITY;
+    for (int i = 0; i < 4; ++i) {
+      float v = (acc[i] + xor_f(acc[i], 8)) * sl2;
+      if (4 * g + i >= nk) v = -INFINITY;
       sc[i] = v;
       tmax = fmaxf(tmax, v);
     }
     tmax = fmaxf(tmax, xor_f(tmax, 16));
     tmax = fmaxf(tmax, xor_f(tmax, 32));
     const float m_new = fmaxf(m_run, tmax);
-    const float corr = exp2f(m_run - m_new);
-    m_run = m_new;
     float psum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      sc[i] = exp2f(sc[i] - m_new);
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_new);
       psum += sc[i];
     }
-    l_run = l_run * corr + psum;
+    if (__any(m_new != m_run)) {  // lazy rescale: skipped when no row's max moved
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= corr;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] *= corr;
+      for (int i = 0; i < 16; ++i) o[i] *= corr;
+    }
+    m_run = m_new;
+    l_run += psum;
 
-    // ---- O^T += V^T P^T
-    if constexpr (VT == F16) {
-      half8 pf;
+    // ---- O^T += V^T P^T (16 keys)
+    if (a.dbg & 4) {
+      o[0][0] += sc[0] + sc[3];
+      (void)vl;
+    } else if constexpr (VT == F16) {
+      half4 pf;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) pf[i] = (n < 8) ? hi_part(sc[i]) : lo_part(sc[i]);
+      for (int i = 0; i < 4; ++i) pf[i] = (n < 8) ? hi_part(sc[i]) : lo_part(sc[i]);
 #pragma unroll
       for (int dt = 0; dt < 16; ++dt)
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v_frag<VT>(vl, 16 * dt + n, g), pf, o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_frag<VT>(vl, 16 * dt + n, g), pf, o[dt], 0, 0, 0);
     } else {
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
-        half8 pf;
+        half4 pf;
+        const float4 dv = *(const float4 *)(dv_t + b * 16 + 4 * g);
+        const float dvv[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int key = (i < 4) ? 4 * g + i : 16 + 4 * g + i - 4;
-          const float pd = sc[i] * scale_of<VT>(vl + key * VS, b);
+        for (int i = 0; i < 4; ++i) {
+          const float pd = sc[i] * dvv[i];
           pf[i] = (n < 8) ? hi_part(pd) : lo_part(pd);
         }
 #pragma unroll
         for (int dd = 0; dd < 2; ++dd) {
           const int dt = 2 * b + dd;
-          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v_frag<VT>(vl, 16 * dt + n, g), pf, o[dt], 0, 0, 0);
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_frag<VT>(vl, 16 * dt + n, g), pf, o[dt], 0, 0, 0);
         }
       }
     }
@@ -385,9 +442,9 @@ __global__ __launch_bounds__(kThreads, (KT == F16 || VT == F16) ? 1 : 2) void de
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[dt][i] += xor_f(o[dt][i], 8);
 
-  // ---- merge the 4 waves through LDS (reuses the tile buffers)
+  // ---- merge the waves through LDS (reuses the tile buffers)
   __syncthreads();
-  float *wm = (float *)smem;                 // [kWaves][kG] m, then l
+  float *wm = (float *)smem;                 // [kWaves][kG] m, then [kWaves][kG] l
   float *wo = wm + 2 * kWaves * kG;          // [kWaves][kG][kHD]
   if (lane < kG) {
     wm[w * kG + lane] = m_run;
@@ -396,18 +453,17 @@ __global__ __launch_bounds__(kThreads, (KT == F16 || VT == F16) ? 1 : 2) void de
   if (n < 8) {
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wo[(w * kG + n) * kHD + 16 * dt + 4 * g + i] = o[dt][i];
+      *(floatx4 *)(wo + (w * kG + n) * kHD + 16 * dt + 4 * g) = o[dt];
   }
   __syncthreads();
-  float *ms = wm + 2 * kWaves * kG + kWaves * kG * kHD;  // [kG] m (natural log units), l, and per-wave weights
+  float *ms = wo + kWaves * kG * kHD;  // [kG] m (ln units), [kG] L, [kWaves][kG] weights
   if (tid < kG) {
     float mm = -INFINITY;
     for (int ww = 0; ww < kWaves; ++ww) mm = fmaxf(mm, wm[ww * kG + tid]);
     float L = 0.0f;
     for (int ww = 0; ww < kWaves; ++ww) {
       const float wt = (mm == -INFINITY) ? 0.0f : exp2f(wm[ww * kG + tid] - mm);
-      ms[3 * kG + ww * kG + tid] = wt;
+      ms[2 * kG + ww * kG + tid] = wt;
       L += wt * wm[kWaves * kG + ww * kG + tid];
     }
     ms[tid] = (mm == -INFINITY) ? -INFINITY : mm * 0.6931471805599453f;  // log2 -> ln units
@@ -416,40 +472,39 @@ __global__ __launch_bounds__(kThreads, (KT == F16 || VT == F16) ? 1 : 2) void de
   __syncthreads();
 
   const int64_t qoff = ((int64_t)tok * a.n_head + h0) * kHD;
-  if (a.n_splits == 1) {
-    for (int i = tid; i < G * kHD; i += kThreads) {
-      const int hh = i / kHD, d = i - hh * kHD;
-      float acc = 0.0f;
+  const int64_t hrow = (int64_t)tok * a.n_head + h0;
+  for (int i = tid; i < G * kHD / 4; i += kThreads) {
+    const int hh = i / (kHD / 4), d = 4 * (i - hh * (kHD / 4));
+    floatx4 acc4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) acc += ms[3 * kG + ww * kG + hh] * wo[(ww * kG + hh) * kHD + d];
+    for (int ww = 0; ww < kWaves; ++ww)
+      acc4 += ms[2 * kG + ww * kG + hh] * *(const floatx4 *)(wo + (ww * kG + hh) * kHD + d);
+    if (a.n_splits == 1) {
       const float L = ms[kG + hh];
-      float o1 = (ms[hh] == -INFINITY) ? 0.0f : acc * ((L > 0.0f) ? 1.0f / L : 0.0f);
-      const int64_t oi = qoff + i;
-      if (a.gate) {
-        const float sg = sigmoid_dev(a.gate[oi]);
-        a.gate[oi] = sg;
-        o1 = o1 * sg;
-      }
-      a.out[oi] = o1;
-    }
-    return;
-  }
-  const int rec = 2 + kHD;
-  for (int i = tid; i < G * rec; i += kThreads) {
-    const int hh = i / rec, c = i - hh * rec;
-    float val;
-    if (c == 0) {
-      val = ms[hh];
-    } else if (c == 1) {
-      val = ms[kG + hh];
-    } else {
-      val = 0.0f;
+      const float inv = (ms[hh] == -INFINITY) ? 0.0f : ((L > 0.0f) ? 1.0f / L : 0.0f);
 #pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) val += ms[3 * kG + ww * kG + hh] * wo[(ww * kG + hh) * kHD + c - 2];
+      for (int k = 0; k < 4; ++k) {
+        float o1 = acc4[k] * inv;
+        const int64_t oi = qoff + hh * kHD + d + k;
+        if (a.gate) {
+          const float sg = sigmoid_dev(a.gate[oi]);
+          a.gate[oi] = sg;
+          o1 = o1 * sg;
+        }
+        a.out[oi] = o1;
+      }
+    } else {
+      *(floatx4 *)(rec_acc(a, hrow + hh, s) + d) = acc4;
     }
-    a.partial[(((int64_t)tok * a.n_head + h0 + hh) * a.n_splits + s) * rec + c] = val;
   }
-  int *flag = (int *)(ms + 8 * kG);
+  if (a.n_splits == 1) return;
+  if (tid < G) {
+    float *ml = rec_ml(a, hrow + tid, s);
+    ml[0] = ms[tid];
+    ml[1] = ms[kG + tid];
+  }
+  int *flag = (int *)(ms + 2 * kG + kWaves * kG);
+  if (a.dbg & 1) return;
   split_tail<kThreads>(a, tok, kvh, hc, h0, G, s, flag, (float *)(flag + 4),
                        (float *)(flag + 4) + kGMaxMerge * kMergeFan);
 }
@@ -458,8 +513,9 @@ namespace {
 
 template <int KT, int VT>
 size_t decode_lds() {
-  const size_t tiles = (size_t)kWaves * wave_lds_bytes<KT, VT>();
-  const size_t merge = (2 * kWaves * kG + kWaves * kG * kHD + 8 * kG + 4) * 4 +
+  using TS = TileShape<KT, VT>;
+  const size_t tiles = (size_t)TS::WAVES * (TS::R * TS::TB + TS::DT);
+  const size_t merge = (2 * TS::WAVES * kG + TS::WAVES * kG * kHD + 2 * kG + TS::WAVES * kG + 4) * 4 +
                        (kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
   return tiles > merge ? tiles : merge;
 }
@@ -467,7 +523,8 @@ size_t decode_lds() {
 template <int KT, int VT>
 hipError_t launch(const AttnArgs &a, int n_tok, hipStream_t st) {
   dim3 grid((unsigned)a.n_splits, (unsigned)(a.n_head_kv * a.n_chunks), (unsigned)n_tok);
-  hipLaunchKernelGGL((decode_mfma_kernel<KT, VT>), grid, dim3(kThreads), (decode_lds<KT, VT>()), st, a);
+  hipLaunchKernelGGL((decode_mfma_kernel<KT, VT>), grid, dim3(64 * TileShape<KT, VT>::WAVES),
+                     (decode_lds<KT, VT>()), st, a);
   return hipGetLastError();
 }
 

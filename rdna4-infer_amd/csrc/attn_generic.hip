@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void attn_generic_kernel(AttnArgs a) {
         store_group4<KT>(x, tid & 7, row, u >> 3);
     }
   }
-  if (a.k_new) __threadfence();
+  if (a.k_new) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   __syncthreads();
 
   const int64_t qoff = ((int64_t)tok * a.n_head + h0) * hd;
@@ -249,12 +249,15 @@ __global__ __launch_bounds__(kThreads) void attn_generic_kernel(AttnArgs a) {
     return;
   }
 
-  // Publish this split's partial: [tok][head][split][2 + hd], then merge.
-  const int rec = 2 + hd;
-  for (int i = tid; i < G * rec; i += kThreads) {
-    const int g = i / rec, c = i - g * rec;
-    const float val = c == 0 ? m_s[g] : (c == 1 ? l_s[g] : q_s[g * hd + c - 2]);
-    a.partial[(((int64_t)tok * a.n_head + h0 + g) * a.n_splits + s) * rec + c] = val;
+  // Publish this split's records, then merge.
+  for (int i = tid; i < G * hd; i += kThreads) {
+    const int hh = i / hd, d = i - hh * hd;
+    rec_acc(a, (int64_t)tok * a.n_head + h0 + hh, s)[d] = q_s[i];
+  }
+  if (tid < G) {
+    float *ml = rec_ml(a, (int64_t)tok * a.n_head + h0 + tid, s);
+    ml[0] = m_s[tid];
+    ml[1] = l_s[tid];
   }
   split_tail<kThreads>(a, tok, kvh, hc, h0, G, s, flag, red, red + kGMaxMerge * kMergeFan);
 }

@@ -21,12 +21,15 @@ struct AttnArgs {
   int n_head, n_head_kv, head_dim;
   float scale;
   int n_splits;           // key splits per (token, kv head)
-  float *partial;         // [n_tok][n_head][n_splits][2 + hd] scratch
-  int64_t l1_offset;      // floats from partial to the level-1 merge records
+  float *partial;         // split records (uncached scratch), layout below
+  // acc [n_tok][n_head][n_splits][hd] at partial; (m, l) [n_tok][n_head][n_splits][2]
+  // at partial + ml0_off; level-1 merge records likewise at acc1_off / ml1_off.
+  int64_t ml0_off, acc1_off, ml1_off;
   unsigned *counters;     // [n_tok][n_head_kv][n_chunks][kCtrStride], zero between launches
   // filled by the launcher
   int n_chunks;
   int k_lds_stride, v_lds_stride;
+  int dbg;  // profiling knob bits (0 in production)
 };
 
 hipError_t attn_generic_launch(int kt, int vt, AttnArgs a, int n_tok, hipStream_t st);

@@ -59,13 +59,14 @@ int get_scratch(Scratch **out) {
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   Scratch &s = g_scratch[dev];
   if (!s.partial) {
-    if (hipMalloc(&s.partial, kPartialFloats * sizeof(float)) != hipSuccess)
+    // Uncached: the split records cross XCDs inside one launch (see merge.hpp).
+    // Allocated once per device and never freed.
+    if (hipExtMallocWithFlags((void **)&s.partial, kPartialFloats * sizeof(float),
+                              hipDeviceMallocUncached) != hipSuccess)
       return fail(RD4_ENOMEM, "scratch allocation failed%s");
     if (hipMalloc(&s.counters, kCounterWords * sizeof(unsigned)) != hipSuccess ||
         hipMemset(s.counters, 0, kCounterWords * sizeof(unsigned)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
-      (void)hipFree(s.partial);
-      s.partial = nullptr;
       return fail(RD4_ENOMEM, "counter allocation failed%s");
     }
   }
@@ -82,12 +83,16 @@ int check_attn_shape(int n_head, int n_head_kv, int head_dim, int kt, int vt) {
   return RD4_OK;
 }
 
-// Splits the GPU wants for `keys` keys of one token: enough CTAs to give every
-// CU several, while keeping at least two 32-key tiles per split.
-int auto_splits(int keys, int ctas_per_split) {
-  if (keys <= 64) return 1;
-  int s = (1024 + ctas_per_split - 1) / ctas_per_split;
-  const int by_keys = (keys + 63) / 64;
+// Splits the GPU wants for `keys` keys of one token: `target` CTAs in total
+// (the MFMA kernel's CTA fills a CU; the generic kernel's takes a quarter of
+// one), and at least `min_keys` keys per split.
+int auto_splits(int keys, int ctas_per_split, int target, int min_keys) {
+  if (const char *e = std::getenv("RD4_DECODE_SPLITS")) {  // tuning override
+    const int v = std::atoi(e);
+    if (v >= 1) return v > kMaxSplits ? kMaxSplits : v;
+  }
+  int s = (target + ctas_per_split - 1) / ctas_per_split;
+  const int by_keys = (keys + min_keys - 1) / min_keys;
   if (s > by_keys) s = by_keys;
   if (s > kMaxSplits) s = kMaxSplits;
   return s < 1 ? 1 : s;
@@ -104,6 +109,14 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   if (!q || !k || !v || !out) return fail(RD4_EINVAL, "null buffer%s");
   const int n_chunks = (n_head / n_head_kv + 7) / 8;
   const int64_t rec = 2 + head_dim;
+  const bool aligned16 = ((((uintptr_t)k) | ((uintptr_t)v)) & 15) == 0;
+  const bool mfma = aligned16 && decode_mfma_supported(kt, vt, n_head, n_head_kv, head_dim);
+  if (splits <= 0) {  // automatic, at least -splits
+    const int min_s = -splits;
+    splits = mfma ? auto_splits(t + 1, n_head_kv * n_chunks, 256, 128)
+                  : auto_splits(t + 1, n_head_kv * n_chunks, 1024, 64);
+    if (splits < min_s) splits = min_s;
+  }
   if (splits < 1) splits = 1;
   if (splits > kMaxSplits) splits = kMaxSplits;
   AttnArgs a{};
@@ -126,18 +139,24 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
     // level-0 + level-1 records must fit; counters too.
     auto floats_for = [&](int S) {
       const int NG = (S + kMergeFan - 1) / kMergeFan;
-      return (int64_t)n_tok * n_head * rec * (S + (NG > 1 ? NG : 0));
+      return (int64_t)n_tok * n_head * (rec + 2) * (S + (NG > 1 ? NG : 0));
     };
     while (splits > 1 && floats_for(splits) > kPartialFloats) splits = (splits + 1) / 2;
     const int64_t ctr_words = (int64_t)n_tok * n_head_kv * n_chunks * kCtrStride;
     if (ctr_words > kCounterWords) splits = 1;
     a.partial = s->partial;
     a.counters = s->counters;
-    a.l1_offset = (int64_t)n_tok * n_head * splits * rec;
+    const int64_t rows = (int64_t)n_tok * n_head;
+    const int NG = (splits + kMergeFan - 1) / kMergeFan;
+    a.ml0_off = rows * splits * head_dim;
+    a.acc1_off = a.ml0_off + rows * splits * 2;
+    a.acc1_off = (a.acc1_off + 3) / 4 * 4;  // 16-byte aligned level-1 records
+    a.ml1_off = a.acc1_off + rows * NG * head_dim;
   }
   a.n_splits = splits;
-  const bool aligned16 = ((((uintptr_t)k) | ((uintptr_t)v)) & 15) == 0;
-  if (aligned16 && decode_mfma_supported(kt, vt, n_head, n_head_kv, head_dim))
+  static const int dbg = [] { const char *e = std::getenv("RD4_DECODE_DBG"); return e ? std::atoi(e) : 0; }();
+  a.dbg = dbg;
+  if (mfma)
     return launched(decode_mfma_launch(kt, vt, a, n_tok, st), "decode kernel");
   return launched(attn_generic_launch(kt, vt, a, n_tok, st), "attention kernel");
 }
@@ -217,10 +236,8 @@ int rd4_attn_decode(const float *q, const void *k, const void *v, float *out, fl
   if (n_splits < 0) return fail(RD4_EINVAL, "n_splits must be >= 0%s");
   int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
   if (rc) return rc;
-  const int cps = n_head_kv * ((n_head / n_head_kv + 7) / 8);
-  const int s = n_splits ? n_splits : auto_splits(t + 1, cps);
   return run_attn(q, k, v, out, gate, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt, vt,
-                  s, (hipStream_t)stream);
+                  n_splits, (hipStream_t)stream);
 }
 
 int rd4_attn_decode_append(const float *q, const float *k_new, const float *v_new, void *k,
@@ -234,10 +251,8 @@ int rd4_attn_decode_append(const float *q, const float *k_new, const float *v_ne
   if (rc) return rc;
   if ((kt >= RD4_KV_Q8_0 && ((uintptr_t)k & 1)) || (vt >= RD4_KV_Q8_0 && ((uintptr_t)v & 1)))
     return fail(RD4_EINVAL, "cache pointers misaligned%s");
-  const int cps = n_head_kv * ((n_head / n_head_kv + 7) / 8);
-  const int s = n_splits ? n_splits : auto_splits(t + 1, cps);
   return run_attn(q, k, v, out, gate, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt, vt,
-                  s, (hipStream_t)stream, k_new, v_new);
+                  n_splits, (hipStream_t)stream, k_new, v_new);
 }
 
 int rd4_attn_launch(const float *q, const void *k, const void *v, float *out, int t, int n_head,
@@ -253,11 +268,8 @@ int rd4_attn_launch_split(const float *q, const void *k, const void *v, float *o
   if (n_splits < 1) return fail(RD4_EINVAL, "n_splits must be >= 1%s");
   int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
   if (rc) return rc;
-  const int cps = n_head_kv * ((n_head / n_head_kv + 7) / 8);
-  int s = auto_splits(t + 1, cps);
-  if (s < n_splits) s = n_splits;
   return run_attn(q, k, v, out, nullptr, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt,
-                  vt, s, (hipStream_t)stream);
+                  vt, -n_splits, (hipStream_t)stream);
 }
 
 int rd4_attn_launch_split_wpb(const float *q, const void *k, const void *v, float *out,

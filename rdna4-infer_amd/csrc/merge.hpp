@@ -9,9 +9,10 @@
 // two-level tree over groups of kMergeFan splits. The last CTA of each group to
 // finish (device-scope counter, reset by that CTA) folds its group's records into
 // one level-1 record; the last group-merger folds the level-1 records into the
-// output. Each merging CTA reads at most kMergeFan records per head, so the
-// serial tail stays short even with 256 splits, and the partials never need a
-// second kernel launch.
+// output. The records live in uncached device memory, so CTAs on different XCDs
+// (whose L2s are not coherent with each other) exchange them with plain 16-byte
+// loads and stores; a writer only waits for its stores to complete before the
+// counter increment, and a merger issues all of its record loads at once.
 #pragma once
 #include "attn_generic.hpp"
 
@@ -19,28 +20,44 @@ namespace rd4 {
 
 constexpr int kMergeFan = 16;
 constexpr int kCtrStride = 1 + kMaxSplits / kMergeFan;  // level-2 + level-1 counters
+constexpr int kGMaxMerge = 8;
+
+// Wait until this thread's vector memory stores are acknowledged; also a
+// compiler barrier for memory.
+__device__ __forceinline__ void stores_done() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ float sigmoid_dev(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Fold n (<= kMergeFan) records per head for G heads. src points at head 0's
-// first record; heads are src_hstride floats apart, records rec floats apart.
-// final: normalize, gate and write a.out/a.gate at qoff; else write one record
-// per head to dst (dst_hstride floats apart). w_s: LDS [kGMaxMerge][kMergeFan],
-// ml_s: LDS [kGMaxMerge][2]. All NT threads must call.
-constexpr int kGMaxMerge = 8;
+// Fold n (<= kMergeFan) records per head for G heads. acc: head 0's first
+// record, heads acc_hs floats apart, records hd floats apart; ml likewise with
+// (m, l) pairs. final: normalize, gate and write a.out/a.gate at qoff; else
+// write one record per head to dacc/dml. w_s: LDS [kGMaxMerge][kMergeFan];
+// ml_s: LDS [kGMaxMerge][2]. All NT threads of the CTA call it.
 template <int NT>
-__device__ __forceinline__ void merge_records(const float *src, int64_t src_hstride, int n, int G,
-                                              int hd, bool final, const AttnArgs &a, int64_t qoff,
-                                              float *dst, int64_t dst_hstride, float *w_s,
-                                              float *ml_s) {
+__device__ __forceinline__ void merge_records(const float *acc, const float *ml, int64_t acc_hs,
+                                              int64_t ml_hs, int n, int G, int hd, bool final,
+                                              const AttnArgs &a, int64_t qoff, float *dacc,
+                                              float *dml, int64_t dacc_hs, int64_t dml_hs,
+                                              float *w_s, float *ml_s) {
   const int tid = threadIdx.x;
-  const int rec = 2 + hd;
+  // Record loads first (one item of 4 dims per thread when G*hd/4 <= NT), so the
+  // (m, l) round trip and the record round trip overlap.
+  const int nq = hd / 4;
+  const int it0 = tid;
+  const bool have0 = it0 < G * nq;
+  const int g0 = have0 ? it0 / nq : 0, d0 = have0 ? 4 * (it0 - g0 * nq) : 0;
+  float4 v0[kMergeFan];
+  {
+    const float *r = acc + g0 * acc_hs + d0;
+#pragma unroll
+    for (int si = 0; si < kMergeFan; ++si)
+      v0[si] = (have0 && si < n) ? *(const float4 *)(r + (int64_t)si * hd) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   if (tid < kGMaxMerge * kMergeFan) {
     const int g = tid / kMergeFan, si = tid % kMergeFan;
     const bool on = g < G && si < n;
-    const float *r = src + g * src_hstride + (int64_t)si * rec;
-    const float ms = on ? r[0] : -INFINITY;
-    const float ls = on ? r[1] : 0.0f;
+    const float ms = on ? ml[g * ml_hs + 2 * si] : -INFINITY;
+    const float ls = on ? ml[g * ml_hs + 2 * si + 1] : 0.0f;
     float mm = ms;
 #pragma unroll
     for (int m = 1; m < kMergeFan; m <<= 1) mm = fmaxf(mm, xor_f(mm, m));
@@ -56,44 +73,64 @@ __device__ __forceinline__ void merge_records(const float *src, int64_t src_hstr
   }
   __syncthreads();
   if (!final && tid < G) {
-    dst[tid * dst_hstride] = ml_s[2 * tid];
-    dst[tid * dst_hstride + 1] = ml_s[2 * tid + 1];
+    dml[tid * dml_hs] = ml_s[2 * tid];
+    dml[tid * dml_hs + 1] = ml_s[2 * tid + 1];
   }
-  for (int i = tid; i < G * hd; i += NT) {
-    const int g = i / hd, d = i - g * hd;
-    const float *r = src + g * src_hstride + 2 + d;
-    float o = 0.0f;
-    for (int si = 0; si < n; ++si) o += r[(int64_t)si * rec] * w_s[g * kMergeFan + si];
+  for (int it = tid; it < G * nq; it += NT) {
+    const int g = it / nq, d = 4 * (it - g * nq);
+    float4 v[kMergeFan];
+    if (it == it0) {
+#pragma unroll
+      for (int si = 0; si < kMergeFan; ++si) v[si] = v0[si];
+    } else {
+      const float *r = acc + g * acc_hs + d;
+#pragma unroll
+      for (int si = 0; si < kMergeFan; ++si)
+        v[si] = si < n ? *(const float4 *)(r + (int64_t)si * hd) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int si = 0; si < kMergeFan; ++si) {
+      const float w = w_s[g * kMergeFan + si];
+      o.x += v[si].x * w;
+      o.y += v[si].y * w;
+      o.z += v[si].z * w;
+      o.w += v[si].w * w;
+    }
     if (final) {
       const float mm = ml_s[2 * g], L = ml_s[2 * g + 1];
-      o = (mm == -INFINITY) ? 0.0f : o * ((L > 0.0f) ? 1.0f / L : 0.0f);
-      const int64_t oi = qoff + i;
-      if (a.gate) {
-        const float sg = sigmoid_dev(a.gate[oi]);
-        a.gate[oi] = sg;
-        o = o * sg;
+      const float inv = (mm == -INFINITY) ? 0.0f : ((L > 0.0f) ? 1.0f / L : 0.0f);
+      float ov[4] = {o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+      const int64_t oi = qoff + (int64_t)g * hd + d;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (a.gate) {
+          const float sg = sigmoid_dev(a.gate[oi + i]);
+          a.gate[oi + i] = sg;
+          ov[i] = ov[i] * sg;
+        }
+        a.out[oi + i] = ov[i];
       }
-      a.out[oi] = o;
     } else {
-      dst[g * dst_hstride + 2 + d] = o;
+      *(float4 *)(dacc + g * dacc_hs + d) = o;
     }
   }
 }
 
-// Called by every CTA after it has written its level-0 record(s) for heads
+// Called by every CTA after it has written its level-0 records for heads
 // h0..h0+G-1 of token tok, split s. flag: LDS int. Returns after the merge (or
-// immediately for CTAs that are not the last of their group).
+// at once for CTAs that are not the last of their group).
 template <int NT>
 __device__ __forceinline__ void split_tail(const AttnArgs &a, int tok, int kvh, int hc, int h0,
                                            int G, int s, int *flag, float *w_s, float *ml_s) {
   const int tid = threadIdx.x;
-  const int hd = a.head_dim, rec = 2 + hd, S = a.n_splits;
+  const int hd = a.head_dim, S = a.n_splits;
   const int NG = (S + kMergeFan - 1) / kMergeFan;
   const int group = s / kMergeFan;
   const int n_in = min(kMergeFan, S - group * kMergeFan);
   unsigned *ctr = a.counters + (((int64_t)tok * a.n_head_kv + kvh) * a.n_chunks + hc) * kCtrStride;
 
-  __threadfence();
+  stores_done();
   __syncthreads();
   if (tid == 0) {
     const unsigned done = atomicAdd(ctr + 1 + group, 1u);
@@ -102,19 +139,22 @@ __device__ __forceinline__ void split_tail(const AttnArgs &a, int tok, int kvh, 
   }
   __syncthreads();
   if (!flag[0]) return;
-  __threadfence();
 
   const int64_t qoff = ((int64_t)tok * a.n_head + h0) * hd;
-  const float *src = a.partial + (((int64_t)tok * a.n_head + h0) * S + group * kMergeFan) * rec;
+  const int64_t hrow = (int64_t)tok * a.n_head + h0;  // first head row of this chunk
+  const float *acc0 = a.partial + (hrow * S + group * kMergeFan) * hd;
+  const float *ml0 = a.partial + a.ml0_off + (hrow * S + group * kMergeFan) * 2;
   if (NG == 1) {
-    merge_records<NT>(src, (int64_t)S * rec, n_in, G, hd, true, a, qoff, nullptr, 0, w_s, ml_s);
+    merge_records<NT>(acc0, ml0, (int64_t)S * hd, (int64_t)S * 2, n_in, G, hd, true, a, qoff,
+                      nullptr, nullptr, 0, 0, w_s, ml_s);
     return;
   }
-  float *l1 = a.partial + (int64_t)a.l1_offset;
-  float *dst = l1 + (((int64_t)tok * a.n_head + h0) * NG + group) * rec;
-  merge_records<NT>(src, (int64_t)S * rec, n_in, G, hd, false, a, qoff, dst, (int64_t)NG * rec,
-                    w_s, ml_s);
-  __threadfence();
+  float *acc1 = a.partial + a.acc1_off + hrow * NG * hd;
+  float *ml1 = a.partial + a.ml1_off + hrow * NG * 2;
+  merge_records<NT>(acc0, ml0, (int64_t)S * hd, (int64_t)S * 2, n_in, G, hd, false, a, qoff,
+                    acc1 + group * hd, ml1 + group * 2, (int64_t)NG * hd, (int64_t)NG * 2, w_s,
+                    ml_s);
+  stores_done();
   __syncthreads();
   if (tid == 0) {
     const unsigned done = atomicAdd(ctr, 1u);
@@ -123,9 +163,16 @@ __device__ __forceinline__ void split_tail(const AttnArgs &a, int tok, int kvh, 
   }
   __syncthreads();
   if (!flag[0]) return;
-  __threadfence();
-  const float *src1 = l1 + ((int64_t)tok * a.n_head + h0) * NG * rec;
-  merge_records<NT>(src1, (int64_t)NG * rec, NG, G, hd, true, a, qoff, nullptr, 0, w_s, ml_s);
+  merge_records<NT>(acc1, ml1, (int64_t)NG * hd, (int64_t)NG * 2, NG, G, hd, true, a, qoff,
+                    nullptr, nullptr, 0, 0, w_s, ml_s);
+}
+
+// Level-0 record of head row `hrow` (= tok * n_head + head), split s.
+__device__ __forceinline__ float *rec_acc(const AttnArgs &a, int64_t hrow, int s) {
+  return a.partial + (hrow * a.n_splits + s) * a.head_dim;
+}
+__device__ __forceinline__ float *rec_ml(const AttnArgs &a, int64_t hrow, int s) {
+  return a.partial + a.ml0_off + (hrow * a.n_splits + s) * 2;
 }
 
 }  // namespace rd4
