@@ -1,5 +1,6 @@
-// Prefill dispatch. First version: the generic split-KV kernel with one CTA per
-// (token, kv head) (positions pos0 + i); f32 queries only.
+// Prefill dispatch: the MFMA kernel (attn_prefill_mfma.hip) for f16 K/V with
+// head_dim 256 and 16-byte aligned buffers; every other shape runs the generic
+// kernel with one CTA per (token, kv head) over keys 0..position.
 #include "prefill.hpp"
 
 namespace rd4 {
@@ -10,6 +11,10 @@ bool prefill_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim) 
 }
 
 hipError_t prefill_launch(int kt, int vt, const PrefillArgs &p, hipStream_t st) {
+  const uintptr_t al = (uintptr_t)p.q | (uintptr_t)p.k | (uintptr_t)p.v | (uintptr_t)p.out |
+                       (uintptr_t)p.gate;
+  if ((al & 15) == 0 && prefill_mfma_supported(kt, vt, p.n_head, p.n_head_kv, p.head_dim))
+    return prefill_mfma_launch(p, st);
   AttnArgs a{};
   a.q = (const float *)p.q;
   a.q_f16 = p.q_f16;

@@ -10,8 +10,8 @@ def to_dev(a, torch, dev):
 
 
 def check_close(got, ref, what=""):
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
     assert np.all(np.isfinite(got)), what + ": non-finite output"
     err = np.abs(got - ref)
     mx = float(err.max()) if err.size else 0.0

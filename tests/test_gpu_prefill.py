@@ -43,3 +43,68 @@ def test_fa2_entry_point(rd4, orc, dev):
     rd4.fa2_prefill(qd, to_dev(k, torch, dev), to_dev(v, torch, dev), qd, to_dev(pos, torch, dev),
                     n - 1, n, nh, nkv, hd, 1 / 16)
     check_close(qd.cpu().numpy(), want, "fa2 in-place")
+
+
+@pytest.mark.parametrize("nh,nkv,pos0,nq,q_f16,gated", [
+    (24, 4, 0, 37, True, True),      # first chunk, ragged row count
+    (16, 2, 50, 129, False, False),  # group 8, f32 queries, no gate
+    (4, 4, 7, 65, True, True),       # group 1 (MHA)
+    (24, 4, 1000, 512, True, False), # the reference's chunk size
+])
+def test_prefill_shapes(rd4, orc, dev, nh, nkv, pos0, nq, q_f16, gated):
+    import torch
+    hd = 256
+    n = pos0 + nq
+    k = orc.store_rows(1, orc.randn(n * nkv * hd, 11))
+    v = orc.store_rows(1, orc.randn(n * nkv * hd, 12))
+    q = orc.randn(nq * nh * hd, 13).reshape(nq, nh, hd)
+    if q_f16:
+        q = q.astype(np.float16).astype(np.float32)
+    pos = np.arange(pos0, n, dtype=np.int32)
+    want = orc.attn_batch(q, k, v, pos, nh, nkv, hd, 1 / 16, 1, 1, threads=8).ravel()
+    g = orc.randn(nq * nh * hd, 14)
+    if gated:
+        _, want = orc.sigmoid_gate(g, want)
+    qd = to_dev(q.astype(np.float16) if q_f16 else q, torch, dev)
+    out = torch.empty(nq * nh * hd, dtype=torch.float32, device=dev)
+    rd4.prefill(qd, to_dev(k, torch, dev), to_dev(v, torch, dev), out, pos0, nh, nkv, hd, 1 / 16, 1, 1,
+                gate=to_dev(g, torch, dev) if gated else None)
+    check_close(out.cpu().numpy(), want, "prefill %d/%d pos0 %d n %d" % (nh, nkv, pos0, nq))
+
+
+def test_prefill_config5_sampled_rows(rd4, orc, dev):
+    """4096 f16 queries at 4096..8191 over 8192 f16 keys,
+    causal, gated; every output row of a sample of tokens vs the oracle."""
+    import torch
+    nh, nkv, hd, pos0, nq = 24, 4, 256, 4096, 4096
+    n = pos0 + nq
+    k = orc.store_rows(1, orc.randn(n * nkv * hd, 21))
+    v = orc.store_rows(1, orc.randn(n * nkv * hd, 22))
+    q = orc.randn(nq * nh * hd, 23).reshape(nq, nh, hd).astype(np.float16)
+    g = orc.randn(nq * nh * hd, 24).reshape(nq, nh, hd)
+    out = torch.empty((nq, nh, hd), dtype=torch.float32, device=dev)
+    gd = to_dev(g, torch, dev)
+    rd4.prefill(to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev), out, pos0, nh, nkv,
+                hd, 1 / 16, 1, 1, gate=gd)
+    got = out.cpu().numpy()
+    rows = np.int32([0, 1, 2, 63, 64, 127, 1000, 2047, 2048, 3333, 4094, 4095])
+    want = orc.attn_batch(q[rows].astype(np.float32), k, v, pos0 + rows, nh, nkv, hd, 1 / 16, 1, 1,
+                          threads=8)
+    _, want = orc.sigmoid_gate(g[rows], want)
+    check_close(got[rows].ravel(), want, "config 5 rows")
+    assert np.all(np.isfinite(got))
+
+
+def test_prefill_mfma_matches_generic(rd4, orc, dev, monkeypatch):
+    import torch
+    nh, nkv, hd, pos0, nq = 24, 4, 256, 333, 300
+    n = pos0 + nq
+    k = to_dev(orc.store_rows(1, orc.randn(n * nkv * hd, 31)), torch, dev)
+    v = to_dev(orc.store_rows(1, orc.randn(n * nkv * hd, 32)), torch, dev)
+    q = to_dev(orc.randn(nq * nh * hd, 33).reshape(nq, nh, hd).astype(np.float16), torch, dev)
+    a = torch.empty(nq * nh * hd, device=dev)
+    b = torch.empty_like(a)
+    rd4.prefill(q, k, v, a, pos0, nh, nkv, hd, 1 / 16, 1, 1)
+    monkeypatch.setenv("RD4_PREFILL_GENERIC", "1")
+    rd4.prefill(q, k, v, b, pos0, nh, nkv, hd, 1 / 16, 1, 1)
+    check_close(a.cpu().numpy(), b.cpu().numpy(), "mfma vs generic")
