@@ -9,13 +9,16 @@
 //
 // Work decomposition: the (query, head) pairs of one kv head form rows
 // r = query * group + head_in_group, so every head of a GQA group shares the K/V
-// tiles. CTA = 4 waves = 128 consecutive rows of one kv head; each wave owns 32
-// rows (two 16-row MFMA slabs). The CTA walks 64-key blocks:
+// tiles. CTA = 8 waves = 128 consecutive rows of one kv head; each wave owns 16
+// rows (one MFMA slab), two waves per SIMD so one wave's softmax overlaps
+// another's MFMAs. The CTA walks 64-key blocks:
 //   * K block (64 x 256 f16) arrives by global->LDS DMA, row-major with the
 //     16-byte chunks of row r XOR-swizzled by r & 15 (conflict-free reads);
-//   * V block is loaded into registers and written to LDS transposed
-//     ([dim][key]) so the PV operand is key-contiguous;
-//   both are double-buffered: block j+1 is in flight while block j computes.
+//   * V block arrives the same way into a raw buffer and is transposed
+//     cooperatively into V^T [dim][key] so the PV operand is key-contiguous;
+//   block j+1's DMA is in flight while block j computes (K double-buffered);
+//   within a block, the next MFMA operand fragments are read from LDS while
+//   the current ones feed the MFMAs.
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_f16 (A = 16 keys x 32 dims of K from
 //     LDS, reused by both slabs; B = the wave's query rows in registers);
 //   * online softmax in registers (exp2 domain, lazy O rescale); the C layout
@@ -37,15 +40,19 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kHD = 256;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kRowsW = 32;                 // rows per wave (2 slabs of 16)
+constexpr int kNSL = 1;                    // 16-row MFMA slabs per wave
+constexpr int kRowsW = 16 * kNSL;          // rows per wave
+constexpr int kNDMA = 2048 / (64 * kWaves); // 16-byte DMA chunks per lane per K (or V) block
 constexpr int kBM = kWaves * kRowsW;       // rows per CTA
 constexpr int kBN = 64;                    // keys per block
 constexpr int kKBytes = kBN * kHD * 2;     // K block, 32 KiB
-constexpr int kVTStride = (kBN + 8) * 2;   // V^T row (one dim) stride in bytes
+constexpr int kVTStride = (kBN + 4) * 2;   // V^T row (one dim) stride: 34 words, bank-spread
 constexpr int kVTBytes = kHD * kVTStride;  // 36 KiB
-constexpr int kStage = kKBytes + kVTBytes;
+constexpr int kVRaw = kBN * kHD * 2;      // raw V block staging (DMA target), 32 KiB
+// LDS: two K stages, one V^T buffer, one raw V buffer
+constexpr int kLdsBytes = 2 * kKBytes + kVTBytes + kVRaw;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ _Float16 h16(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
@@ -59,8 +66,22 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   const int grp = p.n_head / p.n_head_kv;
   const int n_rows = p.n_q * grp;
   const int n_rb = (n_rows + kBM - 1) / kBM;
-  const int rb = n_rb - 1 - (int)blockIdx.x;  // heaviest first
-  const int kvh = blockIdx.y;
+  // XCD-aware order: workgroup L runs on XCD L % 8. When the kv heads divide
+  // the 8 XCDs, each kv head gets 8 / n_head_kv XCDs that take its row blocks
+  // in turn (heaviest first), so an XCD's L2 serves one kv head whose CTAs
+  // sweep the same keys at about the same time.
+  const int total = n_rb * p.n_head_kv;
+  const int L = blockIdx.x;
+  int kvh, rbp;
+  if (8 % p.n_head_kv == 0 && total % 8 == 0) {
+    const int X = 8 / p.n_head_kv, xcd = L % 8, j = L / 8;
+    kvh = xcd % p.n_head_kv;
+    rbp = j * X + xcd / p.n_head_kv;
+  } else {
+    kvh = L / n_rb;
+    rbp = L - kvh * n_rb;
+  }
+  const int rb = n_rb - 1 - rbp;
   const int r0 = rb * kBM;
 
   // Causal limit of a row: last key it may attend.
@@ -91,10 +112,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 
   // ---- this wave's query rows: B operand of S^T (row n of slab s is row
   // r0 + 32w + 16s + n), f16 (f32 queries are rounded to f16)
-  half8 qf[2][8];
-  int lim_row[2];
+  // q is pre-scaled by scale*log2(e) so S comes out in the exp2 domain
+  const float sl2 = p.scale * kLog2e;
+  half8 qf[kNSL][8];
+  int lim_row[kNSL];
 #pragma unroll
-  for (int sl = 0; sl < 2; ++sl) {
+  for (int sl = 0; sl < kNSL; ++sl) {
     const int row = r0 + kRowsW * w + 16 * sl + n;
     lim_row[sl] = limit_of(row);
     const bool on = row < n_rows;
@@ -106,7 +129,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 #pragma unroll
       for (int b = 0; b < 8; ++b) r[b] = *(const u32x4 *)((const uint16_t *)p.q + qoff + 32 * b);
 #pragma unroll
-      for (int b = 0; b < 8; ++b) qf[sl][b] = on ? __builtin_bit_cast(half8, r[b]) : half8{};
+      for (int b = 0; b < 8; ++b) {
+        const half8 h = __builtin_bit_cast(half8, r[b]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[sl][b][i] = on ? (_Float16)((float)h[i] * sl2) : (_Float16)0.0f;
+      }
     } else {
       float4 r[16];
 #pragma unroll
@@ -119,173 +146,251 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
         const float v[8] = {r[2 * b].x, r[2 * b].y, r[2 * b].z, r[2 * b].w,
                             r[2 * b + 1].x, r[2 * b + 1].y, r[2 * b + 1].z, r[2 * b + 1].w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qf[sl][b][i] = on ? (_Float16)v[i] : (_Float16)0.0f;
+        for (int i = 0; i < 8; ++i) qf[sl][b][i] = on ? (_Float16)(v[i] * sl2) : (_Float16)0.0f;
       }
     }
   }
-  const float sl2 = p.scale * kLog2e;
   // The wave's smallest row limit: blocks whose last key is <= it need no mask.
-  int wave_min_lim = min(lim_row[0], lim_row[1]);
+  int wave_min_lim = lim_row[0];
+#pragma unroll
+  for (int sl = 1; sl < kNSL; ++sl) wave_min_lim = min(wave_min_lim, lim_row[sl]);
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) wave_min_lim = min(wave_min_lim, __shfl_xor(wave_min_lim, m, 64));
 
-  floatx4 o[2][16];
+  floatx4 o[kNSL][16];
 #pragma unroll
-  for (int sl = 0; sl < 2; ++sl)
+  for (int sl = 0; sl < kNSL; ++sl)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[sl][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  float m_run[kNSL], l_run[kNSL];
+#pragma unroll
+  for (int sl = 0; sl < kNSL; ++sl) {
+    m_run[sl] = -INFINITY;
+    l_run[sl] = 0.0f;
+  }
 
   // ---- block loads. K: 2048 chunks of 16 B per block = 8 DMA instructions per
   // lane; chunk c -> key c/32, LDS slot c%32 holds global column slot^(key&15).
+  // Per-lane offsets are block-invariant and computed once.
+  int k_goff[kNDMA];  // byte offset of this lane's chunk r from the block's first key
+#pragma unroll
+  for (int r = 0; r < kNDMA; ++r) {
+    const int c = (w * kNDMA + r) * 64 + lane;
+    const int key = c >> 5, slot = c & 31;
+    k_goff[r] = key * (int)kvstride + 16 * (slot ^ (key & 15));
+  }
   auto issue_k = [&](int blk, int stage) {
-    uint8_t *kd = smem + stage * kStage;
+    uint8_t *kd = smem + stage * kKBytes;
     const int j0 = blk * kBN;
+    const uint8_t *src = kbase + (int64_t)j0 * kvstride;
+    if (j0 + kBN - 1 <= kend) {
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int c = (w * 8 + r) * 64 + lane;
-      const int key = c >> 5, slot = c & 31;
-      const int col = slot ^ (key & 15);
-      const int jk = min(j0 + key, kend);  // rows past the range re-read a valid row (masked later)
-      __builtin_amdgcn_global_load_lds((const void *)(kbase + (int64_t)jk * kvstride + 16 * col),
-                                       (lds_void *)(kd + (w * 8 + r) * 1024), 16, 0, 0);
-    }
-  };
-  // V: thread = 4 consecutive keys x 8 dims, two such groups per block.
-  u32x4 vr[2][4];
-  auto load_v = [&](int blk) {
-    const int j0 = blk * kBN;
+      for (int r = 0; r < kNDMA; ++r)
+        __builtin_amdgcn_global_load_lds((const void *)(src + k_goff[r]),
+                                         (lds_void *)(kd + (w * kNDMA + r) * 1024), 16, 0, 0);
+    } else {  // last block: keys past kend re-read a valid row (masked later)
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      const int u = tid + kThreads * gi;      // 0..511
-      const int kq = u >> 5, c = u & 31;      // key quad 0..15, dim chunk 0..31
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int jk = min(j0 + 4 * kq + i, kend);
-        vr[gi][i] = *(const u32x4 *)(vbase + (int64_t)jk * kvstride + 16 * c);
+      for (int r = 0; r < kNDMA; ++r) {
+        const int c = (w * kNDMA + r) * 64 + lane;
+        const int key = c >> 5, slot = c & 31;
+        const int jk = min(j0 + key, kend);
+        __builtin_amdgcn_global_load_lds(
+            (const void *)(kbase + (int64_t)jk * kvstride + 16 * (slot ^ (key & 15))),
+            (lds_void *)(kd + (w * kNDMA + r) * 1024), 16, 0, 0);
       }
     }
   };
-  auto store_vt = [&](int stage) {
-    uint8_t *vt = smem + stage * kStage + kKBytes;
+  // V: the raw block (64 rows x 512 B) arrives by DMA like K (unswizzled), then
+  // each thread transposes 4 keys x 8 dims (two such groups) into V^T [dim][key].
+  uint8_t *const vt = smem + 2 * kKBytes;
+  uint8_t *const vraw = vt + kVTBytes;
+  int v_goff[kNDMA];
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      const int u = tid + kThreads * gi;
-      const int kq = u >> 5, c = u & 31;
+  for (int r = 0; r < kNDMA; ++r) {
+    const int c = (w * kNDMA + r) * 64 + lane;
+    v_goff[r] = (c >> 5) * (int)kvstride + 16 * (c & 31);
+  }
+  auto issue_v = [&](int blk) {
+    const int j0 = blk * kBN;
+    const uint8_t *src = vbase + (int64_t)j0 * kvstride;
+    if (j0 + kBN - 1 <= kend) {
+#pragma unroll
+      for (int r = 0; r < kNDMA; ++r)
+        __builtin_amdgcn_global_load_lds((const void *)(src + v_goff[r]),
+                                         (lds_void *)(vraw + (w * kNDMA + r) * 1024), 16, 0, 0);
+    } else {
+#pragma unroll
+      for (int r = 0; r < kNDMA; ++r) {
+        const int c = (w * kNDMA + r) * 64 + lane;
+        const int jk = min(j0 + (c >> 5), kend);
+        __builtin_amdgcn_global_load_lds((const void *)(vbase + (int64_t)jk * kvstride + 16 * (c & 31)),
+                                         (lds_void *)(vraw + (w * kNDMA + r) * 1024), 16, 0, 0);
+      }
+    }
+  };
+  constexpr int kTG = 512 / kThreads;  // 4-key x 8-dim transpose groups per thread
+  int vr_off[kTG], vt_off[kTG];
+#pragma unroll
+  for (int gi = 0; gi < kTG; ++gi) {
+    const int u = tid + kThreads * gi;
+    const int kq = u & 15, c = u >> 4;  // key quad 0..15 (fastest), dim chunk 0..31
+    vr_off[gi] = 4 * kq * (kHD * 2) + 16 * c;
+    vt_off[gi] = 8 * c * kVTStride + 8 * kq;
+  }
+  auto transpose_v = [&]() {
+#pragma unroll
+    for (int gi = 0; gi < kTG; ++gi) {
+      u32x4 x[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = *(const u32x4 *)(vraw + vr_off[gi] + i * (kHD * 2));
 #pragma unroll
       for (int j = 0; j < 8; ++j) {  // dim 8c + j: keys 4kq..4kq+3
-        const int wsel = j >> 1, hsel = j & 1;
-        const uint32_t a0 = vr[gi][0][wsel], a1 = vr[gi][1][wsel];
-        const uint32_t a2 = vr[gi][2][wsel], a3 = vr[gi][3][wsel];
-        const uint32_t sel = hsel ? 0x07060302u : 0x05040100u;  // high or low halves
-        const uint32_t lo = __builtin_amdgcn_perm(a1, a0, sel);
-        const uint32_t hi = __builtin_amdgcn_perm(a3, a2, sel);
-        *(u32x2 *)(vt + (8 * c + j) * kVTStride + 8 * kq) = u32x2{lo, hi};
+        const int wsel = j >> 1;
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
+        const uint32_t lo = __builtin_amdgcn_perm(x[1][wsel], x[0][wsel], sel);
+        const uint32_t hi = __builtin_amdgcn_perm(x[3][wsel], x[2][wsel], sel);
+        *(u32x2 *)(vt + vt_off[gi] + j * kVTStride) = u32x2{lo, hi};
       }
     }
   };
+  // LDS read offsets of the MFMA operands (block-invariant).
+  // K: key 16kt + n, dims 32b + 8g: slot (4b + g) ^ n = 4(b ^ (n>>2)) + (g ^ (n&3)).
+  int k_loff[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) k_loff[b] = n * (kHD * 2) + 64 * (b ^ (n >> 2)) + 16 * (g ^ (n & 3));
+  const int v_loff = n * kVTStride + 8 * g;  // V^T: dim 16dt + n, keys 32kg + 4g
 
   if (n_blocks > 0) {
     issue_k(0, 0);
-    load_v(0);
-    store_vt(0);
+    issue_v(0);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    transpose_v();
   }
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int st = blk & 1;
     const bool more = blk + 1 < n_blocks;
+    __syncthreads();  // K stage st and V^T of block blk are complete; vraw is free
     if (more) {
       issue_k(blk + 1, st ^ 1);
-      load_v(blk + 1);
-      __asm__ volatile("s_waitcnt vmcnt(16)" ::: "memory");  // block blk's K DMA is done
-    } else {
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      issue_v(blk + 1);
     }
-    __syncthreads();  // K and V^T of block blk visible to all waves
-
-    const uint8_t *kd = smem + st * kStage;
-    const uint8_t *vt = kd + kKBytes;
+    const uint8_t *kd = smem + st * kKBytes;
     const int j0 = blk * kBN;
     const bool need_mask = (j0 + kBN - 1) > wave_min_lim;
 
-    {
-      // ---- S^T for 4 key tiles x 2 slabs
-      floatx4 s[2][4];
+    // ---- S^T for 4 key tiles x 2 slabs; the next tile's K fragments are read
+    // from LDS while the current tile's MFMAs run.
+    floatx4 s[kNSL][4];
+    // fragment f = 8*kt + b of the block: key tile kt, 32-dim step b; a ring of
+    // 2 x 4 fragments keeps the next four reads in flight behind four MFMA pairs
+    u32x4 kb[2][4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        s[0][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        s[1][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        const int key = 16 * kt + n;
-        const uint8_t *krow = kd + key * (kHD * 2);
+    for (int b = 0; b < 4; ++b) kb[0][b] = *(const u32x4 *)(kd + k_loff[b]);
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-          const half8 kf = __builtin_bit_cast(half8, *(const u32x4 *)(krow + 16 * ((4 * b + g) ^ (key & 15))));
-          s[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][b], s[0][kt], 0, 0, 0);
-          s[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[1][b], s[1][kt], 0, 0, 0);
-        }
+    for (int h = 0; h < 8; ++h) {  // half-tile h: kt = h/2, b = 4*(h&1) .. +3
+      if (h < 7) {
+        const int kt1 = (h + 1) >> 1, b1 = 4 * ((h + 1) & 1);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          kb[(h + 1) & 1][b] = *(const u32x4 *)(kd + kt1 * 16 * (kHD * 2) + k_loff[b1 + b]);
       }
-      // ---- online softmax per slab: lane = row n, keys 16kt + 4g + i
-      half8 pf[2][2];
+      const int kt = h >> 1, b0 = 4 * (h & 1);
+      if (b0 == 0) {
 #pragma unroll
-      for (int sl = 0; sl < 2; ++sl) {
-        float tmax = -INFINITY;
+        for (int sl = 0; sl < kNSL; ++sl) s[sl][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+      for (int b = 0; b < 4; ++b) {
+        const half8 kf = __builtin_bit_cast(half8, kb[h & 1][b]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v = s[sl][kt][i] * sl2;
-            if (need_mask && j0 + 16 * kt + 4 * g + i > lim_row[sl]) v = -INFINITY;
-            s[sl][kt][i] = v;
-            tmax = fmaxf(tmax, v);
-          }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run[sl], tmax);
-        // rows with no key yet keep m = -inf; exp2(-inf - -inf) must not be used
-        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-        float psum = 0.0f;
+        for (int sl = 0; sl < kNSL; ++sl)
+          s[sl][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][b0 + b], s[sl][kt], 0, 0, 0);
+      }
+    }
+    // ---- online softmax per slab: lane = row n, keys 16kt + 4g + i
+    half8 pf[kNSL][2];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+    for (int sl = 0; sl < kNSL; ++sl) {
+      float tmax = -INFINITY;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(s[sl][kt][i] - m_use);
-            s[sl][kt][i] = e;
-            psum += e;
-          }
-        if (__any(m_new != m_run[sl])) {
-          const float corr = (m_run[sl] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[sl] - m_use);
-          l_run[sl] *= corr;
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) o[sl][i] *= corr;
+        for (int i = 0; i < 4; ++i) {
+          float v = s[sl][kt][i];
+          if (need_mask && j0 + 16 * kt + 4 * g + i > lim_row[sl]) v = -INFINITY;
+          s[sl][kt][i] = v;
+          tmax = fmaxf(tmax, v);
         }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      // The reference max only moves when the block max exceeds it by more than
+      // 2^8 (p <= 256 stays exact enough in f16 and l, O are f32): most blocks
+      // then skip the O rescale.
+      const bool bump = tmax > m_run[sl] + 8.0f;
+      if (__any(bump)) {
+        const float m_new = bump ? tmax : m_run[sl];
+        const float corr = (m_run[sl] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[sl] - m_new);
+        l_run[sl] *= corr;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[sl][i] *= corr;
         m_run[sl] = m_new;
-        l_run[sl] += psum;
-        // B operand of PV: k-slot 8h + i <-> key 32*kg + 16*(i>>2) + 4h + (i&3)
-#pragma unroll
-        for (int kg = 0; kg < 2; ++kg)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) pf[sl][kg][i] = (_Float16)s[sl][2 * kg + (i >> 2)][i & 3];
       }
-      // ---- O^T += V^T P^T: A = 16 dims x 32 keys of V^T (shared by both slabs)
+      const float m_use = (m_run[sl] == -INFINITY) ? 0.0f : m_run[sl];
+      float psum = 0.0f;
 #pragma unroll
-      for (int kg = 0; kg < 2; ++kg) {
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int dt = 0; dt < 16; ++dt) {
-          const uint8_t *vrow = vt + (16 * dt + n) * kVTStride + 2 * (32 * kg + 4 * g);
+        for (int i = 0; i < 4; ++i) {
+          const float e = __builtin_amdgcn_exp2f(s[sl][kt][i] - m_use);
+          s[sl][kt][i] = e;
+          psum += e;
+        }
+      l_run[sl] += psum;
+      // B operand of PV: k-slot 8h + i <-> key 32*kg + 16*(i>>2) + 4h + (i&3)
+#pragma unroll
+      for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pf[sl][kg][i] = (_Float16)s[sl][2 * kg + (i >> 2)][i & 3];
+    }
+    // ---- O^T += V^T P^T: A = 16 dims x 32 keys of V^T (shared by both slabs);
+    // fragments for the next 4 dim tiles are read while the current 4 run.
+#pragma unroll
+    for (int kg = 0; kg < 2; ++kg) {
+      u32x4 vb[2][2];
+      auto read_vb = [&](int buf, int dt0) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const uint8_t *vrow = vt + 16 * (dt0 + d) * kVTStride + 64 * kg + v_loff;
           const u32x2 lo = *(const u32x2 *)vrow;         // keys 32kg + 4g .. +3
           const u32x2 hi = *(const u32x2 *)(vrow + 32);  // keys 32kg + 16 + 4g .. +3
-          const half8 vf = __builtin_bit_cast(half8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-          o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[0][kg], o[0][dt], 0, 0, 0);
-          o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[1][kg], o[1][dt], 0, 0, 0);
+          vb[buf][d] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+      };
+      read_vb(0, 0);
+#pragma unroll
+      for (int q2 = 0; q2 < 8; ++q2) {
+        if (q2 < 7) read_vb((q2 + 1) & 1, 2 * (q2 + 1));
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const int dt = 2 * q2 + d;
+          const half8 vf = __builtin_bit_cast(half8, vb[q2 & 1][d]);
+#pragma unroll
+          for (int sl = 0; sl < kNSL; ++sl)
+            o[sl][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[sl][kg], o[sl][dt], 0, 0, 0);
         }
       }
     }
-    __syncthreads();  // all waves are done with stage st
-    if (more) store_vt(st ^ 1);
+    if (more) {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA for blk+1 landed
+      __syncthreads();  // every wave is done reading V^T of blk; all DMA landed
+      transpose_v();
+    }
   }
 
   // ---- epilogue: l over the 4 key groups, normalize, gate, store
 #pragma unroll
-  for (int sl = 0; sl < 2; ++sl) {
+  for (int sl = 0; sl < kNSL; ++sl) {
     float L = l_run[sl];
     L += __shfl_xor(L, 16, 64);
     L += __shfl_xor(L, 32, 64);
@@ -322,8 +427,8 @@ bool prefill_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_
 hipError_t prefill_mfma_launch(const PrefillArgs &p, hipStream_t st) {
   const int grp = p.n_head / p.n_head_kv;
   const int n_rb = (p.n_q * grp + kBM - 1) / kBM;
-  dim3 grid((unsigned)n_rb, (unsigned)p.n_head_kv);
-  hipLaunchKernelGGL(prefill_mfma_kernel, grid, dim3(kThreads), (size_t)(2 * kStage), st, p);
+  dim3 grid((unsigned)(n_rb * p.n_head_kv));
+  hipLaunchKernelGGL(prefill_mfma_kernel, grid, dim3(kThreads), (size_t)kLdsBytes, st, p);
   return hipGetLastError();
 }
 

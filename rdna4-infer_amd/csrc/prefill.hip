@@ -1,6 +1,8 @@
 // Prefill dispatch: the MFMA kernel (attn_prefill_mfma.hip) for f16 K/V with
 // head_dim 256 and 16-byte aligned buffers; every other shape runs the generic
 // kernel with one CTA per (token, kv head) over keys 0..position.
+#include <cstdlib>
+
 #include "prefill.hpp"
 
 namespace rd4 {
@@ -13,8 +15,12 @@ bool prefill_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim) 
 hipError_t prefill_launch(int kt, int vt, const PrefillArgs &p, hipStream_t st) {
   const uintptr_t al = (uintptr_t)p.q | (uintptr_t)p.k | (uintptr_t)p.v | (uintptr_t)p.out |
                        (uintptr_t)p.gate;
-  if ((al & 15) == 0 && prefill_mfma_supported(kt, vt, p.n_head, p.n_head_kv, p.head_dim))
-    return prefill_mfma_launch(p, st);
+  if ((al & 15) == 0 && prefill_mfma_supported(kt, vt, p.n_head, p.n_head_kv, p.head_dim)) {
+    static const int dbg = [] { const char *e = std::getenv("RD4_PREFILL_DBG"); return e ? std::atoi(e) : 0; }();
+    PrefillArgs q = p;
+    q.dbg = dbg;
+    return prefill_mfma_launch(q, st);
+  }
   AttnArgs a{};
   a.q = (const float *)p.q;
   a.q_f16 = p.q_f16;

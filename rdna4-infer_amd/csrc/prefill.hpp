@@ -15,6 +15,7 @@ struct PrefillArgs {
   int kmax;           // last key index any query may attend
   int n_q, n_head, n_head_kv, head_dim;
   float scale;
+  int dbg;  // profiling knob bits (0 in production)
 };
 
 bool prefill_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim);
