@@ -200,7 +200,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
       }
     }
   };
-  // V: the raw block (64 rows x 512 B) arrives by DMA like K (unswizzled), then
+  // V: the raw block (64 rows x 512 B) arrives by DMA like K, chunk c of row r
+  // at slot c ^ ((r / 4) & 15) so the transpose's reads spread over the banks; then
   // each thread transposes 4 keys x 8 dims (two such groups) into V^T [dim][key].
   uint8_t *const vt = smem + 2 * kKBytes;
   uint8_t *const vraw = vt + kVTBytes;
@@ -208,7 +209,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 #pragma unroll
   for (int r = 0; r < kNDMA; ++r) {
     const int c = (w * kNDMA + r) * 64 + lane;
-    v_goff[r] = (c >> 5) * (int)kvstride + 16 * (c & 31);
+    const int row = c >> 5;
+    v_goff[r] = row * (int)kvstride + 16 * ((c & 31) ^ ((row >> 2) & 15));
   }
   auto issue_v = [&](int blk) {
     const int j0 = blk * kBN;
@@ -222,8 +224,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 #pragma unroll
       for (int r = 0; r < kNDMA; ++r) {
         const int c = (w * kNDMA + r) * 64 + lane;
-        const int jk = min(j0 + (c >> 5), kend);
-        __builtin_amdgcn_global_load_lds((const void *)(vbase + (int64_t)jk * kvstride + 16 * (c & 31)),
+        const int row = c >> 5;
+        const int jk = min(j0 + row, kend);
+        __builtin_amdgcn_global_load_lds(
+            (const void *)(vbase + (int64_t)jk * kvstride + 16 * ((c & 31) ^ ((row >> 2) & 15))),
                                          (lds_void *)(vraw + (w * kNDMA + r) * 1024), 16, 0, 0);
       }
     }
@@ -234,7 +238,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   for (int gi = 0; gi < kTG; ++gi) {
     const int u = tid + kThreads * gi;
     const int kq = u & 15, c = u >> 4;  // key quad 0..15 (fastest), dim chunk 0..31
-    vr_off[gi] = 4 * kq * (kHD * 2) + 16 * c;
+    vr_off[gi] = 4 * kq * (kHD * 2) + 16 * (c ^ kq);  // raw V rows 4kq..4kq+3 hold chunk c at c ^ kq
     vt_off[gi] = 8 * c * kVTStride + 8 * kq;
   }
   auto transpose_v = [&]() {
