@@ -56,6 +56,16 @@ def make_cache(torch, rd4, t, n, seed, outlier):
     return cache
 
 
+def measured_traffic(workload):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE passes (profiles/traffic.json, copy-calibrated), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)[workload]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def event_loop_ms(torch, fn, steps):
     """Mean ms per call of fn() over `steps` back-to-back calls, from two HIP
     events recorded on the current stream (the stream the library launches on)
@@ -190,7 +200,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode_q8_0",
-                    choices=["decode_q8_0", "decode_f16", "decode_q4_0", "prefill"])
+                    choices=["decode_q8_0", "decode_f16", "decode_q4_0", "prefill", "copy"])
     ap.add_argument("--extra", action="store_true", help="also measure the other configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
@@ -203,6 +213,16 @@ def main():
     rd4.lib()
     if rd4.lib().rd4_init() != 0:
         raise SystemExit("rd4_init failed: " + rd4.lib().rd4_last_error().decode())
+
+    if args.workload == "copy":
+        # Plain device copy of a known size: the calibration run for the
+        # FETCH_SIZE / WRITE_SIZE counters (bytes read = bytes written = 256 MiB).
+        src = torch.ones(64 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        ms = event_loop_ms(torch, lambda: dst.copy_(src), args.steps)
+        print(json.dumps({"workload": "copy", "bytes_read": src.numel() * 4,
+                          "bytes_written": src.numel() * 4, "ms_per_copy": round(ms, 4)}))
+        return
 
     def build(name):
         if name == "decode_q8_0":
@@ -221,7 +241,8 @@ def main():
         value = step_units / (wall_ms * 1e-3) / 1e12
         achieved = dom_units / (dom_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": F16_MFMA_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / F16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(achieved / F16_MFMA_PEAK_TFLOPS, 4),
+                "traffic": measured_traffic(args.workload),
                 "kernel_ms": round(dom_ms, 4)}
         dtype = "f16"
     else:
@@ -231,7 +252,7 @@ def main():
         value = step_units / (wall_ms * 1e-3) / 1e9
         achieved = dom_units / (dom_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload),
                 "kernel_us": round(dom_ms * 1e3, 3)}
         info["us_per_token_layer"] = round(wall_ms * 1e3, 3)
         dtype = "f32"

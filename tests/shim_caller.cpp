@@ -1,0 +1,61 @@
+// A caller written against the reference's rdna4:: API (kv.h, attn.cuh,
+// attn_fa2.cuh, nn.cuh's gate) that builds against the include/rdna4 shims and
+// links librdna4attn. Host-only checks: tables, parse, admission and argument
+// rejection (no kernel runs). Prints "OK" on success.
+#include <cstdio>
+#include <cstring>
+#include <type_traits>
+
+#include "rdna4/attn.cuh"
+#include "rdna4/attn_fa2.cuh"
+#include "rdna4/attn_gate.h"
+
+using namespace rdna4;
+
+// The launchers keep the reference's exact parameter lists.
+static_assert(std::is_same_v<decltype(&attn_launch_split),
+                             bool (*)(const float *, const void *, const void *, float *, float *,
+                                      int, int, int, int, float, KvType, KvType, int,
+                                      hipStream_t)>);
+static_assert(std::is_same_v<decltype(&fa2_prefill_launch),
+                             bool (*)(const float *, const void *, const void *, float *,
+                                      const int *, int, int, int, int, int, int, float,
+                                      hipStream_t)>);
+static_assert(std::is_same_v<decltype(&sigmoid_gate_launch),
+                             bool (*)(float *, float *, std::int64_t, hipStream_t)>);
+
+static int fails = 0;
+#define CHECK(c)                                              \
+  do {                                                        \
+    if (!(c)) {                                               \
+      std::printf("FAIL %s:%d %s\n", __FILE__, __LINE__, #c); \
+      ++fails;                                                \
+    }                                                         \
+  } while (0)
+
+int main() {
+  const KvType all[] = {KvType::F32, KvType::F16, KvType::Q8_0,
+                        KvType::Q4_0, KvType::Q5_0, KvType::Q4_1};
+  const unsigned long long rows[] = {1024, 512, 272, 144, 176, 160};
+  for (int i = 0; i < 6; ++i) {
+    CHECK(kv_row_bytes(all[i], 256) == rows[i]);
+    CHECK((long long)kv_row_bytes(all[i], 256) == rd4_kv_row_bytes((int)all[i], 256));
+    CHECK(kv_bytes_per_elem(all[i]) * 256 == (double)rows[i]);
+    KvType t = KvType::F32;
+    CHECK(kv_type_parse(kKvTypeNames[i].name, &t) == nullptr && t == kKvTypeNames[i].t);
+    CHECK(std::strcmp(kv_type_name(all[i]), kKvTypeNames[i].name) == 0);
+  }
+  KvType t = KvType::Q8_0;
+  CHECK(kv_type_parse("q9_9", &t) != nullptr && t == KvType::Q8_0);
+  CHECK(attn_partial_bytes(24, 256, 32) == (size_t)24 * 32 * (256 + 2) * sizeof(float));
+  CHECK(attn_split_wpb(64) == 8 || attn_split_wpb(64) == 16);
+  CHECK(fa2_prefill_usable(KvType::F16, KvType::F16, 512, 0, 24, 4, 256));
+  CHECK(!fa2_prefill_usable(KvType::Q8_0, KvType::F16, 512, 0, 24, 4, 256));
+  // Argument checks reject before any HIP call: bad head_dim, bad wpb.
+  CHECK(!attn_launch_split(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 24, 4, 255, 1.f,
+                           KvType::F16, KvType::F16, 1));
+  CHECK(!attn_launch_split_wpb(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 24, 4, 256, 1.f,
+                               KvType::F16, KvType::F16, 1, 12));
+  std::printf(fails ? "FAILED %d\n" : "OK\n", fails);
+  return fails ? 1 : 0;
+}
