@@ -206,7 +206,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the decode would shard "
-              "by key ranges with an LSE all-gather; see DESIGN.md)", file=sys.stderr)
+              "by key ranges with an LSE all-gather)", file=sys.stderr)
         sys.exit(2)
     import torch
     rd4 = pkg()

@@ -67,12 +67,21 @@ def lib():
     return _lib
 
 
-def build():
+def _build_module():
     from importlib import util
     spec = util.spec_from_file_location("_rd4_build", os.path.join(HERE, "build.py"))
     mod = util.module_from_spec(spec)
     spec.loader.exec_module(mod)
-    return mod.build(verbose=False)
+    return mod
+
+
+def build():
+    return _build_module().build(verbose=False)
+
+
+def build_shim_check():
+    """Build the test-only device check of the include/rdna4 C++ shims."""
+    return _build_module().build_shim_check()
 
 
 def _check(rc, what):

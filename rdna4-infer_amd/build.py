@@ -54,6 +54,21 @@ def _build(verbose, lib_path):
     return lib_path
 
 
+ROOT = os.path.dirname(HERE)
+SHIM_CHECK_SRC = os.path.join(ROOT, "tests", "shim_kv_device.hip")
+SHIM_CHECK_LIB = os.path.join(ROOT, "tests", "libshimkv.so")
+
+
+def build_shim_check():
+    """Compile the device-side check of the include/rdna4 shims (tests only)."""
+    cmd = [HIPCC, *FLAGS, "-shared", "-I", os.path.join(ROOT, "include"), SHIM_CHECK_SRC,
+           "-o", SHIM_CHECK_LIB]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError("hipcc failed for shim_kv_device.hip:\n" + r.stderr)
+    return SHIM_CHECK_LIB
+
+
 if __name__ == "__main__":
     # python build.py [out.so] [-DNAME=VALUE ...]: variant builds for experiments
     args = sys.argv[1:]

@@ -151,6 +151,76 @@ def test_q4_1_known_answer(orc):
     assert list(q[:5]) == [0, 15, 2, 3, 7] and np.all(q[5:] == 1)
 
 
+def _kvquant_patterns(rows_per=4, hd=256, seed=5):
+    """The 8 row shapes of check_kvquant_gpu.hip:101-137 (uniform, positive,
+    one outlier, constant 0.5, zeros, alternating +-1, gaussian-ish, wide), drawn
+    from numpy instead of the reference's frand."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for p in range(8):
+        u = rng.uniform(-1, 1, size=(rows_per, hd)).astype(np.float32)
+        d = np.arange(hd)
+        x = {0: u, 1: 0.5 * (u + 1), 2: np.where(d == 7, 1.0, 1e-3 * u),
+             3: np.full_like(u, 0.5), 4: np.zeros_like(u),
+             5: np.broadcast_to(np.where(d & 1, -1.0, 1.0), u.shape),
+             6: 0.25 * (u + rng.uniform(-1, 1, size=u.shape) * 3), 7: 100 * u}[p]
+        out.append(np.ascontiguousarray(x, np.float32))
+    return out
+
+
+def test_kvquant_patterns_q8_0_invariants(orc):
+    # Per block: d = f16(amax/127) (IEEE divide, then RNE to f16); the element
+    # holding amax maps to +-127; every code is round(x/d) up to the f16
+    # rounding of d (|x*id - q| <= 0.5 + 127*2^-11); sign(q) = sign(x) or q == 0.
+    for p, x in enumerate(_kvquant_patterns()):
+        b = orc.store_rows(orc.Q8_0, x.ravel()).reshape(-1, 34)
+        xb = x.reshape(-1, 32)
+        amax = np.abs(xb).max(1)
+        d16 = b[:, :2].copy().view(np.float16).ravel()
+        want = (amax / np.float32(127)).astype(np.float32).astype(np.float16)
+        assert np.array_equal(d16.view(np.uint16), want.view(np.uint16)), p
+        q = b[:, 2:].view(np.int8).astype(np.int32)
+        nz = amax > 0
+        arg = np.abs(xb).argmax(1)
+        assert np.all(np.abs(q[np.arange(len(q)), arg][nz]) == 127), p
+        assert np.all(q[~nz] == 0), p
+        dd = (amax / np.float32(127)).astype(np.float64)[:, None]
+        r = np.where(nz[:, None], xb / np.where(dd > 0, dd, 1), 0)
+        assert np.all(np.abs(r - q) <= 0.5 + 1e-6), p
+        assert np.all((q == 0) | (np.sign(q) == np.sign(xb))), p
+        if p == 3:  # constant 0.5: every code 127
+            assert np.all(q == 127)
+        if p == 5:  # alternating: +-127
+            assert np.all(np.abs(q) == 127)
+
+
+def test_kvquant_patterns_q4_0_invariants(orc):
+    # Per block: the signed max v (first of equal magnitudes) gives d = v/-8, so
+    # v itself codes to nibble 0 (dequant -8d = v exactly); nibbles in [0,15];
+    # dequant error <= one step |d| (the +8.5 truncation rounds half up, and the
+    # clamp at 15 costs at most one step on the side opposite to v).
+    for p, x in enumerate(_kvquant_patterns()):
+        flat = x.ravel()
+        b = orc.store_rows(orc.Q4_0, flat).reshape(-1, 18)
+        xb = flat.reshape(-1, 32)
+        arg = np.abs(xb).argmax(1)  # numpy argmax: first occurrence
+        v = xb[np.arange(len(xb)), arg]
+        d16 = b[:, :2].copy().view(np.float16).astype(np.float32).ravel()
+        want = (v / np.float32(-8)).astype(np.float32).astype(np.float16).astype(np.float32)
+        assert np.array_equal(d16, want), p
+        nib = np.concatenate([b[:, 2:] & 15, b[:, 2:] >> 4], 1).astype(np.int32)
+        nz = v != 0
+        assert np.all(nib[np.arange(len(nib)), arg][nz] == 0), p
+        assert np.all(nib[~nz] == 8), p
+        y = orc.load_rows(orc.Q4_0, b.ravel(), flat.size).reshape(-1, 32)
+        step = np.abs(d16)[:, None]
+        assert np.all(np.abs(y - xb) <= step * (1 + 2.0 ** -10) + 1e-6), p
+        if p == 3:  # constant 0.5: d = -1/16, every x*id = -8 -> nibble 0
+            assert np.all(nib == 0) and np.all(d16 == -0.0625)
+        if p == 5:  # +1 first -> d = -1/8: +1 -> 0, -1 -> 16.5 -> clamp 15
+            assert np.all(nib[:, 0::2] == 0) and np.all(nib[:, 1::2] == 15)
+
+
 @pytest.mark.parametrize("t", [2, 3, 4, 5])
 def test_quant_roundtrip_error_bound(orc, t):
     # dequant(quant(x)) is within one quantization step d (q4_1: d) of x, per block

@@ -23,3 +23,37 @@ def test_reference_api_caller_builds_and_runs(rd4, tmp_path):
     subprocess.run(cmd, check=True, capture_output=True, text=True)
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hd", [256, 96])
+def test_shim_device_readers_bit_exact(orc, dev, hd):
+    """rdna4::kv_load<> and kv_load8<> of the shim (built into tests/libshimkv.so)
+    return the oracle's dequant bits (kv.h:174-368) for every type."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    so = os.path.join(ROOT, "tests", "libshimkv.so")
+    if not os.path.exists(so):
+        pytest.fail("tests/libshimkv.so is not built: run __graft_entry__.build()")
+    L = ctypes.CDLL(so)
+    L.shim_kv_read_rows.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    n_rows = 64
+    x = orc.randn(n_rows * hd, 77) * 2
+    x[5::hd] *= 8
+    x[: 2 * hd] = 0.0
+    for t in range(6):
+        b = orc.store_rows(t, x)
+        want = orc.load_rows(t, b, x.size)
+        bd = torch.from_numpy(b).to(dev)
+        for use8 in (0, 1):
+            out = torch.full((n_rows * hd,), float("nan"), dtype=torch.float32, device=dev)
+            rc = L.shim_kv_read_rows(t, bd.data_ptr(), out.data_ptr(), n_rows, hd, use8,
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            assert rc == 0
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (t, use8)
