@@ -40,6 +40,9 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+#ifndef RD4_DEC_AUX
+#define RD4_DEC_AUX 0
+#endif
 constexpr int kHD = 256;     // head_dim of this kernel
 constexpr int kTile = 16;    // keys per wave tile
 constexpr int kG = 8;        // query heads per CTA (MFMA rows 0-7 hi, 8-15 lo)
@@ -119,70 +122,101 @@ __device__ __forceinline__ uint32_t nib2_to_h2(uint32_t v) {
   return __builtin_bit_cast(uint32_t, x);
 }
 
-// A operand of S^T = K Q^T for one 16-key half and one 32-dim block: lane
-// (key = l%16, g = l/16) gets dims 32b + 8g .. +7 of its key, as f16.
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const uint32_t *)p; }
+
+// Dim of head_dim held in k-slot j of lane group g (lanes 16g..16g+15) for the
+// 32-dim block b of the S^T = K Q^T product. Any order within a block is a
+// valid MFMA contraction as long as K and Q use the same one; it is chosen so
+// that every lane reads its K bytes with aligned 32-bit LDS loads. Quantized
+// blocks start 2 bytes past a 4-byte boundary in every other block (34- and
+// 18-byte blocks); there the lane group that would straddle the row's edges
+// takes the block's first two and last two values instead. Pairs (j, j+1)
+// with j even are always two consecutive dims starting at an even dim.
 template <int KT>
-__device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g, int n_of_row) {
+__host__ __device__ constexpr int k_dim(int b, int g, int j) {
+  if (KT == F16 || (b & 1)) {
+    if (KT == Q4_0) return 32 * b + 16 * (g >> 1) + 8 * (g & 1) + j;
+    return 32 * b + 8 * g + j;
+  }
+  if (KT == Q8_0) {
+    if (g < 3) return 32 * b + 8 * g + 2 + j;
+    return 32 * b + (j < 4 ? 26 + j : j == 4 ? 0 : j == 5 ? 1 : j == 6 ? 30 : 31);
+  }
+  // Q4_0: low nibbles (g < 2) hold elements 0..15, high nibbles 16..31
+  const int base = 32 * b + 16 * (g >> 1);
+  if ((g & 1) == 0) return base + 2 + j;
+  return base + (j < 4 ? 10 + j : j == 4 ? 0 : j == 5 ? 1 : j == 6 ? 14 : 15);
+}
+
+// Bytes (sel-chosen pair) of v -> two f16 holding the same signed integers:
+// 0x6400 | (byte ^ 0x80) is the f16 1024 + byte + 128; subtracting 1152 is exact.
+__device__ __forceinline__ uint32_t i8pair_to_h2(uint32_t v, uint32_t sel) {
+  const uint32_t w = __builtin_amdgcn_perm(0u, v, sel) ^ 0x64806480u;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w) + c);
+}
+// Low nibbles of the two bytes sel picks -> two f16 of (nibble - 8).
+__device__ __forceinline__ uint32_t nibpair_to_h2(uint32_t v, uint32_t sel) {
+  const uint32_t w = (__builtin_amdgcn_perm(0u, v, sel) & 0x000f000fu) | 0x64006400u;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 c = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w) + c);
+}
+
+// A operand of S^T = K Q^T for block b: lane (key = l%16, g = l/16) gets the
+// 8 dims k_dim<KT>(b, g, 0..7) of its key as f16. sel_edge is the per-lane
+// v_perm selector that gathers the edge bytes in the unaligned blocks
+// (0x05040302 in the edge lane group, identity 0x07060504 elsewhere).
+template <int KT>
+__device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g, int n_of_row,
+                                        uint32_t sel_edge) {
   u32x4 r;
   if constexpr (KT == F16) {
     r = *(const u32x4 *)(krow + 16 * ((4 * b + g) ^ n_of_row));
-  } else if constexpr (KT == Q8_0) {
-    const uint8_t *p = krow + 34 * b + 2 + 8 * g;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = i8x2_to_h2(lds_u16(p + 2 * i));
-  } else {  // Q4_0: element j < 16 is the low nibble of qs[j], j >= 16 the high nibble of qs[j-16]
-    const uint8_t *p = krow + 18 * b + 2 + 8 * (g & 1);
-    const int sh = (g & 2) ? 4 : 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t v = lds_u16(p + 2 * i) >> sh;  // byte0 -> bits 0-3, byte1 -> bits 8-11
-      r[i] = nib2_to_h2((v & 0xfu) | ((v & 0xf00u) << 8));
+  } else {
+    constexpr int BB = block_bytes(KT);
+    const int gg = KT == Q8_0 ? g : (g & 1);  // q4_0: lane groups g and g^2 read the same bytes
+    uint32_t x, y;
+    if (b & 1) {
+      x = lds_u32(krow + BB * b + 2 + 8 * gg);
+      y = lds_u32(krow + BB * b + 6 + 8 * gg);
+    } else {
+      x = lds_u32(krow + BB * b + 4 + 8 * gg);
+      y = __builtin_amdgcn_perm(lds_u32(krow + BB * b + 8 + 8 * gg), lds_u32(krow + BB * b), sel_edge);
+    }
+    if constexpr (KT == Q8_0) {
+      r[0] = i8pair_to_h2(x, 0x0c010c00u);
+      r[1] = i8pair_to_h2(x, 0x0c030c02u);
+      r[2] = i8pair_to_h2(y, 0x0c010c00u);
+      r[3] = i8pair_to_h2(y, 0x0c030c02u);
+    } else {
+      const int sh = (g & 2) ? 4 : 0;
+      x >>= sh;
+      y >>= sh;
+      r[0] = nibpair_to_h2(x, 0x0c010c00u);
+      r[1] = nibpair_to_h2(x, 0x0c030c02u);
+      r[2] = nibpair_to_h2(y, 0x0c010c00u);
+      r[3] = nibpair_to_h2(y, 0x0c030c02u);
     }
   }
   return __builtin_bit_cast(half8, r);
 }
 
-// A operand of O^T = V^T P^T (v_mfma_f32_16x16x16_f16) for dim d (this lane's)
-// and keys 4g..4g+3 of the tile, as f16.
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Dim of head_dim that row r' (0..15) of PV MFMA t (0..15) accumulates. The V
+// operand lane with MFMA row r reads whole aligned words of its 4 keys:
+//   f16:  16-byte chunk r + 16h (dims 8(r + 16h) .. +7), one MFMA per dim, t = 8h + e;
+//   q8_0: the 2 bytes at dims 32b + 2r, +1 of block b, t = 2b + e;
+//   q4_0: byte r of block b (element r low nibble, r + 16 high), t = 2b + e;
+// so every MFMA's rows lie in one quantization block and share one P' operand.
 template <int VT>
-__device__ __forceinline__ half4 v_frag(const uint8_t *vt, int d, int g) {
-  constexpr int vs = rowb<VT>();
-  const uint8_t *p0 = vt + 4 * g * vs;
-  uint32_t e[4];
-  uint32_t r0, r1;
-  if constexpr (VT == F16) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      e[i] = lds_u16(p0 + i * vs + 16 * ((d >> 3) ^ ((4 * g + i) & 15)) + 2 * (d & 7));
-    r0 = e[0] | (e[1] << 16);
-    r1 = e[2] | (e[3] << 16);
-  } else if constexpr (VT == Q8_0) {
-    // bytes land in the low byte of 16-bit halves; 0x64 | b^0x80 per half is
-    // the f16 1024 + b + 128, so one xor and one packed add give b exactly
-    const int off = 34 * (d >> 5) + 2 + (d & 31);
-    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-    u16x2 a0, a1;
-    a0.x = p0[off];
-    a0.y = p0[vs + off];
-    a1.x = p0[2 * vs + off];
-    a1.y = p0[3 * vs + off];
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    r0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_bit_cast(uint32_t, a0) ^ 0x64806480u) + c);
-    r1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_bit_cast(uint32_t, a1) ^ 0x64806480u) + c);
-    (void)e;
-  } else {
-    const int j = d & 31;
-    const int off = 18 * (d >> 5) + 2 + (j & 15);
-    const int sh = (j & 16) ? 4 : 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) e[i] = (lds_u8(p0 + i * vs + off) >> sh) & 0xfu;
-    r0 = nib2_to_h2(e[0] | (e[1] << 16));
-    r1 = nib2_to_h2(e[2] | (e[3] << 16));
-  }
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(half4, u32x2{r0, r1});
+__host__ __device__ constexpr int v_dim(int t, int r) {
+  return VT == F16 ? 8 * (r + 16 * (t >> 3)) + (t & 7)
+         : VT == Q8_0 ? 32 * (t >> 1) + 2 * r + (t & 1)
+                      : 32 * (t >> 1) + r + 16 * (t & 1);
 }
 
 template <int T>
@@ -193,6 +227,47 @@ __device__ __forceinline__ float scale_of(const uint8_t *row, int b) {
 // hi/lo f16 pair of an f32 (x = hi + lo to ~2^-22 relative).
 __device__ __forceinline__ _Float16 hi_part(float x) { return (_Float16)x; }
 __device__ __forceinline__ _Float16 lo_part(float x) { return (_Float16)(x - (float)(_Float16)x); }
+
+// P operand of the PV product for two keys: x_i = p_i * d_i split across the
+// MFMA rows, f16(x) in rows n < 8 and the f16 remainder x - f16(x) in rows
+// n >= 8 (lo_mask = all ones there, 0 elsewhere). The remainder is a fused
+// multiply-add of the exact product, so hi + lo carries x to ~2^-22.
+__device__ __forceinline__ uint32_t split_prod2(float p0, float d0, float p1, float d1,
+                                                uint32_t lo_mask) {
+  // v_fma_mix{lo,hi}_f16 evaluate p*d (+ an f16 operand) in one fused step and
+  // write one f16 half each: two instructions per pair for hi, two for the
+  // remainder, one AND to zero the subtrahend in the hi rows. The compiler's
+  // hazard tracking does not see into inline asm, so the sequence pads its
+  // own wait states: p may come straight from v_exp_f32 (a transcendental
+  // result read by a VALU op) and the result feeds an MFMA operand (a VALU
+  // write read by an MFMA); s_nop 1 covers two wait states at each end.
+#if RD4_DEC_PSPLIT_C
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const float x0 = p0 * d0, x1 = p1 * d1;
+  const h2 rr = {lo_mask ? lo_part(x0) : hi_part(x0), lo_mask ? lo_part(x1) : hi_part(x1)};
+  return __builtin_bit_cast(uint32_t, rr);
+#endif
+  uint32_t hi, r;
+  __asm__("s_nop 1\n\t"
+          "v_fma_mixlo_f16 %0, %1, %2, 0\n\t"
+          "v_fma_mixhi_f16 %0, %3, %4, 0"
+          : "=&v"(hi)
+          : "v"(p0), "v"(d0), "v"(p1), "v"(d1));
+  const uint32_t m = hi & lo_mask;
+  __asm__("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,0,1]\n\t"
+          "v_fma_mixhi_f16 %0, %4, %5, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+          "s_nop 1"
+          : "=&v"(r)
+          : "v"(p0), "v"(d0), "v"(m), "v"(p1), "v"(d1));
+  return r;
+}
+// Online-softmax reference max: moved only when a row's new scores exceed it
+// by more than kRescaleLog2 (probabilities stay <= 2^8 against a stale max),
+// so the O rescale and the cross-lane max are rare instead of per tile.
+#ifndef RD4_DEC_THRESH
+#define RD4_DEC_THRESH 8.0f
+#endif
+constexpr float kRescaleLog2 = RD4_DEC_THRESH;
 
 }  // namespace
 
@@ -228,66 +303,25 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const uint8_t *vbase = a.v + (int64_t)kvh * rowb<VT>();
 
   // Fused append: the CTA owning key t writes the new K/V row of its kv head
-  // (8-lane groups per 32-element block, the store kernel's quantizer).
-  if (a.k_new && j_begin <= t && t < j_end && tid < 128) {
-    const bool isv = tid >= 64;
-    const int u = tid & 63;
-    const float *src = (isv ? a.v_new : a.k_new) + (int64_t)kvh * kHD + 4 * u;
-    float x[4] = {src[0], src[1], src[2], src[3]};
-    uint8_t *row = (uint8_t *)(isv ? vbase : kbase) + (int64_t)t * (isv ? vstride : kstride);
-    if (isv)
-      store_group4<VT>(x, u & 7, row, u >> 3);
-    else
-      store_group4<KT>(x, u & 7, row, u >> 3);
-  }
-  // the new row reaches this CU's L1 before any wave loads it (workgroup scope only)
-  if (a.k_new) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-  __syncthreads();
-
-  // Query fragment (B operand of S^T = K Q^T): row n is head n (hi) or n-8 (lo).
-  // All of this lane's query loads are issued before any is used.
-  half8 qf[8];
-  {
-    const int hh = n & 7;
-    const bool on = hh < G;
-    const int64_t qoff = (((int64_t)tok * a.n_head + h0 + (on ? hh : 0)) * kHD) + 8 * g;
-    float qv[8][8];
-    if (a.q_f16) {
-      u32x4 r[8];
-#pragma unroll
-      for (int b = 0; b < 8; ++b) r[b] = *(const u32x4 *)((const uint16_t *)a.q + qoff + 32 * b);
-#pragma unroll
-      for (int b = 0; b < 8; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          qv[b][2 * i] = h2f((uint16_t)r[b][i]);
-          qv[b][2 * i + 1] = h2f((uint16_t)(r[b][i] >> 16));
-        }
-    } else {
-      float4 r[16];
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        r[2 * b] = *(const float4 *)(a.q + qoff + 32 * b);
-        r[2 * b + 1] = *(const float4 *)(a.q + qoff + 32 * b + 4);
-      }
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        qv[b][0] = r[2 * b].x; qv[b][1] = r[2 * b].y; qv[b][2] = r[2 * b].z; qv[b][3] = r[2 * b].w;
-        qv[b][4] = r[2 * b + 1].x; qv[b][5] = r[2 * b + 1].y; qv[b][6] = r[2 * b + 1].z; qv[b][7] = r[2 * b + 1].w;
-      }
+  // (8-lane groups per 32-element block, the store kernel's quantizer) before
+  // any of its tiles is requested; every other CTA starts its loads at once.
+  const bool owns_new = a.k_new && j_begin <= t && t < j_end;
+  if (owns_new) {
+    if (tid < 128) {
+      const bool isv = tid >= 64;
+      const int u = tid & 63;
+      const float *src = (isv ? a.v_new : a.k_new) + (int64_t)kvh * kHD + 4 * u;
+      float x[4] = {src[0], src[1], src[2], src[3]};
+      uint8_t *row = (uint8_t *)(isv ? vbase : kbase) + (int64_t)t * (isv ? vstride : kstride);
+      if (isv)
+        store_group4<VT>(x, u & 7, row, u >> 3);
+      else
+        store_group4<KT>(x, u & 7, row, u >> 3);
     }
-#pragma unroll
-    for (int b = 0; b < 8; ++b)
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        qf[b][i] = on ? ((n < 8) ? hi_part(qv[b][i]) : lo_part(qv[b][i])) : (_Float16)0.0f;
+    // the new row reaches this CU's L1 before any wave loads it (workgroup
+    // scope; the barrier after the query staging orders it for the other waves)
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   }
-  const float sl2 = a.scale * kLog2e;
-
-  floatx4 o[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.0f;
 
   // ---- async tile ring: stage i of this wave at ring + (i % R) * TB
   uint8_t *ring = smem + w * (R * TB + DT);
@@ -295,8 +329,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   float *dv_t = dk_t + (KT != F16 ? 128 : 0);              // [8][16] V scales (quantized V)
   const int n_tiles_all = (j_end - j_begin + kTile - 1) / kTile;
   const int my_tiles = (a.dbg & 32) ? 0 : (n_tiles_all > w ? (n_tiles_all - w + kWaves - 1) / kWaves : 0);
-  // Global source of this lane's chunk in load instruction r of a full tile:
+  // Global source of this lane's chunk in load instruction r of a tile:
   // byte offset from the tile's K (or V) base, with the f16 swizzle applied.
+  // Rows past the tile's last key (partial tiles) re-read the tile's first row.
   auto src_of = [&](int r, int nk, const uint8_t *kt0, const uint8_t *vt0) -> const uint8_t * {
     const int c = lane + 64 * r;
     if (c < KCH) {
@@ -309,20 +344,108 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     const int col = swz<VT>(row, slot);
     return vt0 + (row < nk ? row * (int)vstride + 16 * col : 16 * col);
   };
+  // Full tiles use offsets computed once: instructions whose 64 chunks are all
+  // K (or all V) address from a wave-uniform base.
+  int goff[NI];
+#pragma unroll
+  for (int r = 0; r < NI; ++r) {
+    const int c = lane + 64 * r;
+    if (c < KCH) {
+      const int row = c / KC, slot = c - row * KC;
+      goff[r] = row * (int)kstride + 16 * swz<KT>(row, slot);
+    } else {
+      const int cv = c < KCH + VCH ? c - KCH : 0;
+      const int row = cv / VC, slot = cv - row * VC;
+      goff[r] = row * (int)vstride + 16 * swz<VT>(row, slot);
+    }
+  }
   auto issue = [&](int i) {  // i-th tile of this wave
+    if (a.dbg & 2048) return;
     const int j0 = j_begin + (w + i * kWaves) * kTile;
     const int nk = min(kTile, j_end - j0);
     const uint8_t *kt0 = kbase + (int64_t)j0 * kstride;
     const uint8_t *vt0 = vbase + (int64_t)j0 * vstride;
     uint8_t *st = ring + (i % R) * TB;
+    if (nk == kTile) {
 #pragma unroll
-    for (int r = 0; r < NI; ++r)
-      __builtin_amdgcn_global_load_lds((const void *)src_of(r, nk, kt0, vt0),
-                                       (lds_void *)(st + 1024 * r), 16, 0, 0);
+      for (int r = 0; r < NI; ++r) {
+        const uint8_t *base = (64 * r + 63 < KCH) ? kt0 : (64 * r >= KCH) ? vt0
+                              : (lane + 64 * r < KCH ? kt0 : vt0);
+        __builtin_amdgcn_global_load_lds((const void *)(base + goff[r]), (lds_void *)(st + 1024 * r),
+                                         16, 0, RD4_DEC_AUX);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < NI; ++r)
+        __builtin_amdgcn_global_load_lds((const void *)src_of(r, nk, kt0, vt0),
+                                         (lds_void *)(st + 1024 * r), 16, 0, RD4_DEC_AUX);
+    }
   };
+  if (!owns_new) {
 #pragma unroll
-  for (int i = 0; i < R - 1; ++i)
-    if (i < my_tiles) issue(i);
+    for (int i = 0; i < R - 1; ++i)
+      if (i < my_tiles) issue(i);  // first tiles in flight before the query loads
+  }
+
+  // The chunk's G query rows are read from global memory once per CTA (one
+  // 16-byte load per thread) and staged in LDS past the tile rings: per-wave
+  // loads of the same rows from all CTAs would hammer a few L2 channels.
+  float *q_lds = (float *)(smem + kWaves * (R * TB + DT));
+  {
+    const int64_t q0 = ((int64_t)tok * a.n_head + h0) * kHD;
+    if (a.q_f16) {
+      for (int i = tid; i < G * kHD / 8; i += kThreads)
+        ((u32x4 *)q_lds)[i] = *(const u32x4 *)((const uint16_t *)a.q + q0 + 8 * i);
+    } else {
+      for (int i = tid; i < G * kHD / 4; i += kThreads)
+        ((float4 *)q_lds)[i] = *(const float4 *)(a.q + q0 + 4 * i);
+    }
+  }
+  __syncthreads();
+  if (owns_new) {
+#pragma unroll
+    for (int i = 0; i < R - 1; ++i)
+      if (i < my_tiles) issue(i);
+  }
+
+  // Query fragment (B operand of S^T = K Q^T): row n is head n (hi) or n-8
+  // (lo); k-slot j of lane group g holds dim k_dim<KT>(b, g, j), read as
+  // consecutive pairs.
+  half8 qf[8];
+  {
+    const int hh = n & 7;
+    const bool on = hh < G;
+    const int qrow = (on ? hh : 0) * kHD;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int d0 = qrow + k_dim<KT>(b, g, 2 * jj);
+        float x0, x1;
+        if (a.q_f16) {
+          const uint32_t u = *(const uint32_t *)((const uint16_t *)q_lds + d0);
+          x0 = h2f((uint16_t)u);
+          x1 = h2f((uint16_t)(u >> 16));
+        } else {
+          const float2 f = *(const float2 *)(q_lds + d0);
+          x0 = f.x;
+          x1 = f.y;
+        }
+        qf[b][2 * jj] = on ? ((n < 8) ? hi_part(x0) : lo_part(x0)) : (_Float16)0.0f;
+        qf[b][2 * jj + 1] = on ? ((n < 8) ? hi_part(x1) : lo_part(x1)) : (_Float16)0.0f;
+      }
+    }
+  }
+  const float sl2 = a.scale * kLog2e;
+  const uint32_t lo_mask = n >= 8 ? 0xffffffffu : 0u;
+  // edge gather of the unaligned quantized-K blocks: lane group 3 (q8_0) or
+  // the odd lane groups (q4_0) take the block's first and last byte pairs
+  const uint32_t sel_edge = (KT == Q8_0 ? g == 3 : (g & 1) == 1) ? 0x05040302u : 0x07060504u;
+
+  floatx4 o[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
 
   for (int i = 0; i < my_tiles; ++i) {
     const int nk = min(kTile, j_end - (j_begin + (w + i * kWaves) * kTile));
@@ -361,12 +484,12 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       if constexpr (KT == F16) {
 #pragma unroll
         for (int b = 0; b < 8; ++b)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n), qf[b], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), qf[b], acc, 0, 0, 0);
       } else {
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
           const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-          const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n), qf[b], z, 0, 0, 0);
+          const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), qf[b], z, 0, 0, 0);
           const float4 dk = *(const float4 *)(dk_t + b * 16 + 4 * g);
           acc[0] = fmaf(dk.x, c[0], acc[0]);
           acc[1] = fmaf(dk.y, c[1], acc[1]);
@@ -375,32 +498,38 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         }
       }
     }
-    // rows n and n^8 are the hi and lo halves of the same head
+    // Rows n and n^8 are the hi and lo halves of the same head. (A DPP
+    // row_ror:8 add was tried here; the compiler's DPP combine fed acc[0] to
+    // all four adds, so the exchange stays a plain lane shuffle.)
     float sc[4];
-    float tmax = -INFINITY;
+    bool over = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v = (acc[i] + xor_f(acc[i], 8)) * sl2;
+      const float other = xor_f(acc[i], 8);
+      float v = (acc[i] + other) * sl2;
       if (4 * g + i >= nk) v = -INFINITY;
       sc[i] = v;
-      tmax = fmaxf(tmax, v);
+      over |= v > m_run + kRescaleLog2;
     }
-    tmax = fmaxf(tmax, xor_f(tmax, 16));
-    tmax = fmaxf(tmax, xor_f(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    float psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_new);
-      psum += sc[i];
-    }
-    if (__any(m_new != m_run)) {  // lazy rescale: skipped when no row's max moved
+    // The reference max moves only when some score passed it by the threshold
+    // (a wave vote); only then is the tile's row max reduced across lanes.
+    if (__any(over)) {
+      float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      tmax = fmaxf(tmax, xor_f(tmax, 16));
+      tmax = fmaxf(tmax, xor_f(tmax, 32));
+      const float m_new = fmaxf(m_run, tmax);
       const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= corr;
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[i] *= corr;
+      m_run = m_new;
     }
-    m_run = m_new;
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);
+      psum += sc[i];
+    }
     l_run += psum;
 
     // ---- O^T += V^T P^T (16 keys)
@@ -408,27 +537,61 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       o[0][0] += sc[0] + sc[3];
       (void)vl;
     } else if constexpr (VT == F16) {
-      half4 pf;
+      const half4 pf = __builtin_bit_cast(
+          half4, u32x2{split_prod2(sc[0], 1.0f, sc[1], 1.0f, lo_mask),
+                       split_prod2(sc[2], 1.0f, sc[3], 1.0f, lo_mask)});
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pf[i] = (n < 8) ? hi_part(sc[i]) : lo_part(sc[i]);
+      for (int h = 0; h < 2; ++h) {
+        // 16-byte chunk n + 16h (dims 8(n + 16h) .. +7) of the lane's 4 keys
+        u32x4 ch[4];
 #pragma unroll
-      for (int dt = 0; dt < 16; ++dt)
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_frag<VT>(vl, 16 * dt + n, g), pf, o[dt], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          const int row = 4 * g + i;
+          ch[i] = *(const u32x4 *)(vl + row * VS + 16 * ((n ^ (row & 15)) + 16 * h));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          const uint32_t lo = __builtin_amdgcn_perm(ch[1][e >> 1], ch[0][e >> 1], sel);
+          const uint32_t hi = __builtin_amdgcn_perm(ch[3][e >> 1], ch[2][e >> 1], sel);
+          o[8 * h + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{lo, hi}),
+                                                              pf, o[8 * h + e], 0, 0, 0);
+        }
+      }
     } else {
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
-        half4 pf;
         const float4 dv = *(const float4 *)(dv_t + b * 16 + 4 * g);
-        const float dvv[4] = {dv.x, dv.y, dv.z, dv.w};
+        const half4 pf = __builtin_bit_cast(
+            half4, u32x2{split_prod2(sc[0], dv.x, sc[1], dv.y, lo_mask),
+                         split_prod2(sc[2], dv.z, sc[3], dv.w, lo_mask)});
+        uint32_t u[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float pd = sc[i] * dvv[i];
-          pf[i] = (n < 8) ? hi_part(pd) : lo_part(pd);
+          const uint8_t *vrow = vl + (4 * g + i) * VS + block_bytes(VT) * b + 2;
+          u[i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
         }
+        // [key0, key1] and [key2, key3] bytes of the lane's 2-dim (q8_0) or
+        // 2-nibble (q4_0) word, one MFMA per dim
+        const uint32_t w01_0 = __builtin_amdgcn_perm(u[1], u[0], 0x0c040c00u);
+        const uint32_t w23_0 = __builtin_amdgcn_perm(u[3], u[2], 0x0c040c00u);
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-        for (int dd = 0; dd < 2; ++dd) {
-          const int dt = 2 * b + dd;
-          o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(v_frag<VT>(vl, 16 * dt + n, g), pf, o[dt], 0, 0, 0);
+        for (int e = 0; e < 2; ++e) {
+          uint32_t a01, a23;
+          if constexpr (VT == Q8_0) {
+            const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
+            const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+            a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) ^ 0x64806480u) + c);
+            a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) ^ 0x64806480u) + c);
+          } else {
+            const h2 c = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+            const int sh = 4 * e;
+            a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ((w01_0 >> sh) & 0x000f000fu) | 0x64006400u) + c);
+            a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ((w23_0 >> sh) & 0x000f000fu) | 0x64006400u) + c);
+          }
+          o[2 * b + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{a01, a23}),
+                                                              pf, o[2 * b + e], 0, 0, 0);
         }
       }
     }
@@ -451,23 +614,48 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     wm[kWaves * kG + w * kG + lane] = l_run;
   }
   if (n < 8) {
+    // o[t][i] holds dim v_dim<VT>(t, 4g + i); written back as 4-dim runs
+    float *dst = wo + (w * kG + n) * kHD;
+    if constexpr (VT == F16) {
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt)
-      *(floatx4 *)(wo + (w * kG + n) * kHD + 16 * dt + 4 * g) = o[dt];
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = v_dim<VT>(8 * h, 4 * g + i);
+          *(floatx4 *)(dst + d0) = floatx4{o[8 * h][i], o[8 * h + 1][i], o[8 * h + 2][i], o[8 * h + 3][i]};
+          *(floatx4 *)(dst + d0 + 4) = floatx4{o[8 * h + 4][i], o[8 * h + 5][i], o[8 * h + 6][i], o[8 * h + 7][i]};
+        }
+    } else if constexpr (VT == Q8_0) {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const int d0 = v_dim<VT>(2 * b, 4 * g);
+        *(floatx4 *)(dst + d0) = floatx4{o[2 * b][0], o[2 * b + 1][0], o[2 * b][1], o[2 * b + 1][1]};
+        *(floatx4 *)(dst + d0 + 4) = floatx4{o[2 * b][2], o[2 * b + 1][2], o[2 * b][3], o[2 * b + 1][3]};
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) *(floatx4 *)(dst + v_dim<VT>(t, 4 * g)) = o[t];
+    }
   }
   __syncthreads();
   float *ms = wo + kWaves * kG * kHD;  // [kG] m (ln units), [kG] L, [kWaves][kG] weights
-  if (tid < kG) {
-    float mm = -INFINITY;
-    for (int ww = 0; ww < kWaves; ++ww) mm = fmaxf(mm, wm[ww * kG + tid]);
-    float L = 0.0f;
-    for (int ww = 0; ww < kWaves; ++ww) {
-      const float wt = (mm == -INFINITY) ? 0.0f : exp2f(wm[ww * kG + tid] - mm);
-      ms[2 * kG + ww * kG + tid] = wt;
-      L += wt * wm[kWaves * kG + ww * kG + tid];
+  if (tid < kWaves * kG) {
+    // thread (wave ww, head hh); the max and the weighted sum run over ww
+    // (lane bits 3..) with lane exchanges, no serial loop
+    const int hh = tid % kG, ww = tid / kG;
+    const float mw = wm[ww * kG + hh];
+    float mm = mw;
+#pragma unroll
+    for (int x = kG; x < kWaves * kG; x <<= 1) mm = fmaxf(mm, xor_f(mm, x));
+    const float wt = (mm == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - mm);
+    float L = wt * wm[kWaves * kG + ww * kG + hh];
+#pragma unroll
+    for (int x = kG; x < kWaves * kG; x <<= 1) L += xor_f(L, x);
+    ms[2 * kG + ww * kG + hh] = wt;
+    if (ww == 0) {
+      ms[hh] = (mm == -INFINITY) ? -INFINITY : mm * 0.6931471805599453f;  // log2 -> ln units
+      ms[kG + hh] = L;
     }
-    ms[tid] = (mm == -INFINITY) ? -INFINITY : mm * 0.6931471805599453f;  // log2 -> ln units
-    ms[kG + tid] = L;
   }
   __syncthreads();
 
@@ -504,7 +692,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     ml[1] = ms[kG + tid];
   }
   int *flag = (int *)(ms + 2 * kG + kWaves * kG);
-  if (a.dbg & 1) return;
+  if (a.ext_merge || (a.dbg & 1)) return;
   split_tail<kThreads>(a, tok, kvh, hc, h0, G, s, flag, (float *)(flag + 4),
                        (float *)(flag + 4) + kGMaxMerge * kMergeFan);
 }
@@ -514,7 +702,7 @@ namespace {
 template <int KT, int VT>
 size_t decode_lds() {
   using TS = TileShape<KT, VT>;
-  const size_t tiles = (size_t)TS::WAVES * (TS::R * TS::TB + TS::DT);
+  const size_t tiles = (size_t)TS::WAVES * (TS::R * TS::TB + TS::DT) + kG * kHD * sizeof(float);
   const size_t merge = (2 * TS::WAVES * kG + TS::WAVES * kG * kHD + 2 * kG + TS::WAVES * kG + 4) * 4 +
                        (kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
   return tiles > merge ? tiles : merge;
@@ -542,13 +730,23 @@ bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_d
 hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hipStream_t st) {
   AttnArgs a = a0;
   a.n_chunks = (a.n_head / a.n_head_kv + kG - 1) / kG;
+  // Split records are merged by a second, short launch: a kernel boundary makes
+  // them visible for about one launch gap, where an in-kernel tree pays a
+  // device-scope atomic plus a record round trip per level.
+  static const bool tree = [] {
+    const char *e = std::getenv("RD4_DECODE_MERGE");
+    return e && std::atoi(e) == 2;
+  }();
+  a.ext_merge = (a.n_splits > 1 && !tree) ? 1 : 0;
+  hipError_t err = hipErrorInvalidValue;
 #define RD4_D(K, V) \
-  if (kt == K && vt == V) return launch<K, V>(a, n_tok, st);
+  if (kt == K && vt == V) err = launch<K, V>(a, n_tok, st);
   RD4_D(F16, F16) RD4_D(F16, Q8_0) RD4_D(F16, Q4_0)
   RD4_D(Q8_0, F16) RD4_D(Q8_0, Q8_0) RD4_D(Q8_0, Q4_0)
   RD4_D(Q4_0, F16) RD4_D(Q4_0, Q8_0) RD4_D(Q4_0, Q4_0)
 #undef RD4_D
-  return hipErrorInvalidValue;
+  if (err != hipSuccess || !a.ext_merge) return err;
+  return merge_splits_launch(a, n_tok, st);
 }
 
 }  // namespace rd4

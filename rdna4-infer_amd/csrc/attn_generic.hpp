@@ -29,8 +29,16 @@ struct AttnArgs {
   // filled by the launcher
   int n_chunks;
   int k_lds_stride, v_lds_stride;
-  int dbg;  // profiling knob bits (0 in production)
+  int ext_merge;  // 1: the kernel only writes level-0 records; merge_splits_launch merges
+  // Profiling knob (env RD4_DECODE_DBG, 0 in production), MFMA decode kernel:
+  // 1 skip the split merge, 2 skip the QK product, 4 skip the PV product,
+  // 32 no key tiles, 2048 no tile loads (compute on stale LDS).
+  int dbg;
 };
+
+// Merge the level-0 split records of n_tok tokens into out (and apply the gate):
+// one short kernel after the split kernel on the same stream.
+hipError_t merge_splits_launch(const AttnArgs &a, int n_tok, hipStream_t st);
 
 hipError_t attn_generic_launch(int kt, int vt, AttnArgs a, int n_tok, hipStream_t st);
 size_t generic_lds_bytes(int kt, int vt, int hd, int n_splits);
