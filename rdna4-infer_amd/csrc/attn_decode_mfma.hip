@@ -40,10 +40,14 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+#ifndef RD4_DEC_TRACE
+#define RD4_DEC_TRACE 0
+#endif
 #ifndef RD4_DEC_AUX
 #define RD4_DEC_AUX 0
 #endif
 constexpr int kHD = 256;     // head_dim of this kernel
+constexpr int kRowPad = kHD + 4;  // LDS row stride (floats) of per-head rows: spreads banks
 constexpr int kTile = 16;    // keys per wave tile
 constexpr int kG = 8;        // query heads per CTA (MFMA rows 0-7 hi, 8-15 lo)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -78,14 +82,14 @@ __device__ __forceinline__ int swz(int row, int col) {
   return T == F16 ? (col ^ (row & 15)) : col;
 }
 
-// Tile image in LDS: the tile's K rows then V rows, contiguous 16-byte chunks,
-// padded to whole 64-chunk load instructions.
+// Tile image in LDS: the tile's K rows then V rows, contiguous 16-byte chunks
+// (the last load instruction of a tile runs with its surplus lanes off).
 template <int KT, int VT>
 struct TileShape {
   static constexpr int KC = chunks_per_row<KT>(), VC = chunks_per_row<VT>();
   static constexpr int KCH = kTile * KC, VCH = kTile * VC;
   static constexpr int NI = (KCH + VCH + 63) / 64;  // load instructions per tile
-  static constexpr int TB = NI * 1024;              // bytes per ring stage
+  static constexpr int TB = (KCH + VCH) * 16;       // bytes per ring stage
   // per-wave f32 scale tables [block][key] for the quantized K and V of a tile
   static constexpr int DT = (KT != F16 ? 512 : 0) + (VT != F16 ? 512 : 0);
 #ifndef RD4_DEC_WAVES_SMALL
@@ -286,6 +290,20 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const int tok = blockIdx.z;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
+#if RD4_DEC_TRACE
+  // timestamps of CTA (0,0): slot [w][point] in a.out as u64 (diagnostic builds only)
+  int tpos = 0;
+#define RD4_TP()                                                                        \
+  do {                                                                                  \
+    if (blockIdx.x == 0 && blockIdx.y == 0 && lane == 0 && tpos < 60)                   \
+      ((unsigned long long *)a.out)[w * 64 + tpos++] = __builtin_amdgcn_s_memtime();    \
+  } while (0)
+#else
+#define RD4_TP() \
+  do {           \
+  } while (0)
+#endif
+  RD4_TP();
   const int grp = a.n_head / a.n_head_kv;
   const int h0 = kvh * grp + hc * kG;
   const int G = min(kG, grp - hc * kG);
@@ -371,37 +389,51 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       for (int r = 0; r < NI; ++r) {
         const uint8_t *base = (64 * r + 63 < KCH) ? kt0 : (64 * r >= KCH) ? vt0
                               : (lane + 64 * r < KCH ? kt0 : vt0);
-        __builtin_amdgcn_global_load_lds((const void *)(base + goff[r]), (lds_void *)(st + 1024 * r),
-                                         16, 0, RD4_DEC_AUX);
+        if (64 * r + 63 < KCH + VCH || lane + 64 * r < KCH + VCH)
+          __builtin_amdgcn_global_load_lds((const void *)(base + goff[r]), (lds_void *)(st + 1024 * r),
+                                           16, 0, RD4_DEC_AUX);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < NI; ++r)
-        __builtin_amdgcn_global_load_lds((const void *)src_of(r, nk, kt0, vt0),
-                                         (lds_void *)(st + 1024 * r), 16, 0, RD4_DEC_AUX);
+        if (64 * r + 63 < KCH + VCH || lane + 64 * r < KCH + VCH)
+          __builtin_amdgcn_global_load_lds((const void *)src_of(r, nk, kt0, vt0),
+                                           (lds_void *)(st + 1024 * r), 16, 0, RD4_DEC_AUX);
     }
   };
+  // The chunk's G query rows are copied into LDS once per CTA by the same
+  // global->LDS DMA, issued before any tile so they are not queued behind the
+  // tiles; rows are padded by 16 bytes so the per-row fragment reads below do
+  // not collide in one bank.
+  uint8_t *q_lds = smem + kWaves * (R * TB + DT);
+  const int qcw = a.q_f16 ? kHD / 8 : kHD / 4;  // 16-byte chunks per query row
+  const int qsb = 16 * (qcw + 1);               // padded row stride in bytes
+  auto issue_q = [&]() {  // one load instruction per 64 chunks, spread over the waves
+    if (a.dbg & 2048) return;
+    for (int base = 64 * w; base < G * (qcw + 1); base += 64 * kWaves) {
+      const int idx = base + lane, r = idx / (qcw + 1), c = idx - r * (qcw + 1);
+      if (r < G && c < qcw) {
+        const uint8_t *src = (const uint8_t *)a.q +
+                             (((int64_t)tok * a.n_head + h0 + r) * kHD) * (a.q_f16 ? 2 : 4) + 16 * c;
+        __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(q_lds + 16 * base), 16, 0, 0);
+      }
+    }
+  };
+  issue_q();
   if (!owns_new) {
 #pragma unroll
     for (int i = 0; i < R - 1; ++i)
-      if (i < my_tiles) issue(i);  // first tiles in flight before the query loads
+      if (i < my_tiles) issue(i);  // first tiles in flight right behind the query rows
   }
-
-  // The chunk's G query rows are read from global memory once per CTA (one
-  // 16-byte load per thread) and staged in LDS past the tile rings: per-wave
-  // loads of the same rows from all CTAs would hammer a few L2 channels.
-  float *q_lds = (float *)(smem + kWaves * (R * TB + DT));
+  // this wave's query chunk has landed once at most the tile loads issued after it remain
   {
-    const int64_t q0 = ((int64_t)tok * a.n_head + h0) * kHD;
-    if (a.q_f16) {
-      for (int i = tid; i < G * kHD / 8; i += kThreads)
-        ((u32x4 *)q_lds)[i] = *(const u32x4 *)((const uint16_t *)a.q + q0 + 8 * i);
-    } else {
-      for (int i = tid; i < G * kHD / 4; i += kThreads)
-        ((float4 *)q_lds)[i] = *(const float4 *)(a.q + q0 + 4 * i);
-    }
+    const int after = owns_new ? 0 : min(R - 1, my_tiles);
+    if (after >= 2) wait_vm<2 * NI>();
+    else if (after == 1) wait_vm<NI>();
+    else wait_vm<0>();
   }
   __syncthreads();
+  RD4_TP();
   if (owns_new) {
 #pragma unroll
     for (int i = 0; i < R - 1; ++i)
@@ -409,35 +441,44 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   }
 
   // Query fragment (B operand of S^T = K Q^T): row n is head n (hi) or n-8
-  // (lo); k-slot j of lane group g holds dim k_dim<KT>(b, g, j), read as
-  // consecutive pairs.
+  // (lo); k-slot j of lane group g holds dim k_dim<KT>(b, g, j). Every wave
+  // needs the same 8 fragments, so wave w converts blocks w, w + kWaves, ...
+  // once and the CTA exchanges them through LDS (over the query rows).
+  const uint32_t lo_mask = n >= 8 ? 0xffffffffu : 0u;
   half8 qf[8];
   {
     const int hh = n & 7;
     const bool on = hh < G;
-    const int qrow = (on ? hh : 0) * kHD;
+    const uint8_t *qrow = q_lds + (on ? hh : 0) * qsb;
+    u32x4 mine[8 / kWaves];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int m = 0; m < 8 / kWaves; ++m) {
+      const int b = w + kWaves * m;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int d0 = qrow + k_dim<KT>(b, g, 2 * jj);
+        const int d0 = k_dim<KT>(b, g, 2 * jj);
         float x0, x1;
         if (a.q_f16) {
-          const uint32_t u = *(const uint32_t *)((const uint16_t *)q_lds + d0);
+          const uint32_t u = *(const uint32_t *)(qrow + 2 * d0);
           x0 = h2f((uint16_t)u);
           x1 = h2f((uint16_t)(u >> 16));
         } else {
-          const float2 f = *(const float2 *)(q_lds + d0);
+          const float2 f = *(const float2 *)(qrow + 4 * d0);
           x0 = f.x;
           x1 = f.y;
         }
-        qf[b][2 * jj] = on ? ((n < 8) ? hi_part(x0) : lo_part(x0)) : (_Float16)0.0f;
-        qf[b][2 * jj + 1] = on ? ((n < 8) ? hi_part(x1) : lo_part(x1)) : (_Float16)0.0f;
+        mine[m][jj] = on ? split_prod2(x0, 1.0f, x1, 1.0f, lo_mask) : 0u;
       }
     }
+    __syncthreads();  // every wave has read the query rows
+    u32x4 *qf_lds = (u32x4 *)q_lds;  // [block][lane]
+#pragma unroll
+    for (int m = 0; m < 8 / kWaves; ++m) qf_lds[(w + kWaves * m) * 64 + lane] = mine[m];
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 8; ++b) qf[b] = __builtin_bit_cast(half8, qf_lds[b * 64 + lane]);
   }
   const float sl2 = a.scale * kLog2e;
-  const uint32_t lo_mask = n >= 8 ? 0xffffffffu : 0u;
   // edge gather of the unaligned quantized-K blocks: lane group 3 (q8_0) or
   // the odd lane groups (q4_0) take the block's first and last byte pairs
   const uint32_t sel_edge = (KT == Q8_0 ? g == 3 : (g & 1) == 1) ? 0x05040302u : 0x07060504u;
@@ -447,7 +488,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   for (int i = 0; i < 16; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
 
+  RD4_TP();
   for (int i = 0; i < my_tiles; ++i) {
+    RD4_TP();
     const int nk = min(kTile, j_end - (j_begin + (w + i * kWaves) * kTile));
     if (i + R - 1 < my_tiles) {
       // the stage being refilled was read by the previous iteration: those reads are done
@@ -461,6 +504,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     else if (after == 1) wait_vm<NI>();
     else wait_vm<0>();
     wave_sync();
+    RD4_TP();
     const uint8_t *kl = ring + (i % R) * TB;
     const uint8_t *vl = kl + KCH * 16;
     if constexpr (DT > 0) {  // f16 scales of the tile -> f32 tables, once per tile
@@ -475,6 +519,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       wave_sync();
     }
 
+    RD4_TP();
     // ---- S^T = K Q^T: lane holds keys 4g..4g+3 of row n
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
     if (a.dbg & 2) {
@@ -498,6 +543,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         }
       }
     }
+    RD4_TP();
     // Rows n and n^8 are the hi and lo halves of the same head. (A DPP
     // row_ror:8 add was tried here; the compiler's DPP combine fed acc[0] to
     // all four adds, so the exchange stays a plain lane shuffle.)
@@ -532,6 +578,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     }
     l_run += psum;
 
+    RD4_TP();
     // ---- O^T += V^T P^T (16 keys)
     if (a.dbg & 4) {
       o[0][0] += sc[0] + sc[3];
@@ -597,25 +644,23 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     }
   }
 
-  // ---- wave state: head n&7; hi+lo rows summed, l summed over the 4 key groups
+  RD4_TP();
+  // ---- wave state: l summed over the 4 key groups; the hi (n < 8) and lo
+  // (n >= 8) rows of O go to LDS as separate rows and are added by the reader
   l_run += xor_f(l_run, 16);
   l_run += xor_f(l_run, 32);
-#pragma unroll
-  for (int dt = 0; dt < 16; ++dt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[dt][i] += xor_f(o[dt][i], 8);
 
   // ---- merge the waves through LDS (reuses the tile buffers)
   __syncthreads();
   float *wm = (float *)smem;                 // [kWaves][kG] m, then [kWaves][kG] l
-  float *wo = wm + 2 * kWaves * kG;          // [kWaves][kG][kHD]
+  float *wo = wm + 2 * kWaves * kG;          // [kWaves][16 rows][kRowPad]
   if (lane < kG) {
     wm[w * kG + lane] = m_run;
     wm[kWaves * kG + w * kG + lane] = l_run;
   }
-  if (n < 8) {
+  {
     // o[t][i] holds dim v_dim<VT>(t, 4g + i); written back as 4-dim runs
-    float *dst = wo + (w * kG + n) * kHD;
+    float *dst = wo + (w * 16 + n) * kRowPad;
     if constexpr (VT == F16) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
@@ -638,7 +683,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     }
   }
   __syncthreads();
-  float *ms = wo + kWaves * kG * kHD;  // [kG] m (ln units), [kG] L, [kWaves][kG] weights
+  RD4_TP();
+  float *ms = wo + kWaves * 16 * kRowPad;  // [kG] m (ln units), [kG] L, [kWaves][kG] weights
   if (tid < kWaves * kG) {
     // thread (wave ww, head hh); the max and the weighted sum run over ww
     // (lane bits 3..) with lane exchanges, no serial loop
@@ -666,7 +712,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     floatx4 acc4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ww = 0; ww < kWaves; ++ww)
-      acc4 += ms[2 * kG + ww * kG + hh] * *(const floatx4 *)(wo + (ww * kG + hh) * kHD + d);
+      acc4 += ms[2 * kG + ww * kG + hh] * (*(const floatx4 *)(wo + (ww * 16 + hh) * kRowPad + d) +
+                                           *(const floatx4 *)(wo + (ww * 16 + hh + 8) * kRowPad + d));
     if (a.n_splits == 1) {
       const float L = ms[kG + hh];
       const float inv = (ms[hh] == -INFINITY) ? 0.0f : ((L > 0.0f) ? 1.0f / L : 0.0f);
@@ -685,6 +732,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       *(floatx4 *)(rec_acc(a, hrow + hh, s) + d) = acc4;
     }
   }
+  RD4_TP();
   if (a.n_splits == 1) return;
   if (tid < G) {
     float *ml = rec_ml(a, hrow + tid, s);
@@ -702,8 +750,8 @@ namespace {
 template <int KT, int VT>
 size_t decode_lds() {
   using TS = TileShape<KT, VT>;
-  const size_t tiles = (size_t)TS::WAVES * (TS::R * TS::TB + TS::DT) + kG * kHD * sizeof(float);
-  const size_t merge = (2 * TS::WAVES * kG + TS::WAVES * kG * kHD + 2 * kG + TS::WAVES * kG + 4) * 4 +
+  const size_t tiles = (size_t)TS::WAVES * (TS::R * TS::TB + TS::DT) + kG * (kHD * 4 + 16);
+  const size_t merge = (2 * TS::WAVES * kG + TS::WAVES * 16 * kRowPad + 2 * kG + TS::WAVES * kG + 4) * 4 +
                        (kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
   return tiles > merge ? tiles : merge;
 }

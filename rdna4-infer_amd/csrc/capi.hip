@@ -109,7 +109,7 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   if (!q || !k || !v || !out) return fail(RD4_EINVAL, "null buffer%s");
   const int n_chunks = (n_head / n_head_kv + 7) / 8;
   const int64_t rec = 2 + head_dim;
-  const bool aligned16 = ((((uintptr_t)k) | ((uintptr_t)v)) & 15) == 0;
+  const bool aligned16 = ((((uintptr_t)k) | ((uintptr_t)v) | ((uintptr_t)q)) & 15) == 0;
   const bool mfma = aligned16 && decode_mfma_supported(kt, vt, n_head, n_head_kv, head_dim);
   if (splits <= 0) {  // automatic, at least -splits
     const int min_s = -splits;
