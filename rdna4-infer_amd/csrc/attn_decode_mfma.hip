@@ -775,17 +775,22 @@ bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_d
          n_head % n_head_kv == 0;
 }
 
-hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hipStream_t st) {
-  AttnArgs a = a0;
-  a.n_chunks = (a.n_head / a.n_head_kv + kG - 1) / kG;
+bool decode_mfma_ext_merge() {
   // Split records are merged by a second, short launch: a kernel boundary makes
   // them visible for about one launch gap, where an in-kernel tree pays a
-  // device-scope atomic plus a record round trip per level.
+  // device-scope atomic plus a record round trip per level (RD4_DECODE_MERGE=2
+  // selects the tree, for measurements).
   static const bool tree = [] {
     const char *e = std::getenv("RD4_DECODE_MERGE");
     return e && std::atoi(e) == 2;
   }();
-  a.ext_merge = (a.n_splits > 1 && !tree) ? 1 : 0;
+  return !tree;
+}
+
+hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hipStream_t st) {
+  AttnArgs a = a0;
+  a.n_chunks = (a.n_head / a.n_head_kv + kG - 1) / kG;
+  a.ext_merge = (a.n_splits > 1 && decode_mfma_ext_merge()) ? 1 : 0;
   hipError_t err = hipErrorInvalidValue;
 #define RD4_D(K, V) \
   if (kt == K && vt == V) err = launch<K, V>(a, n_tok, st);

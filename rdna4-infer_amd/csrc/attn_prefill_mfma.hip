@@ -14,9 +14,11 @@
 // another's MFMAs. The CTA walks 64-key blocks:
 //   * K block (64 x 256 f16) arrives by global->LDS DMA, row-major with the
 //     16-byte chunks of row r XOR-swizzled by r & 15 (conflict-free reads);
-//   * V block arrives the same way into a raw buffer and is transposed
-//     cooperatively into V^T [dim][key] so the PV operand is key-contiguous;
-//   block j+1's DMA is in flight while block j computes (K double-buffered);
+//   * V block arrives the same way, same swizzle; the PV operand (16 dims x
+//     8 keys per lane group) is read straight out of it with the gfx950
+//     transposing LDS load (ds_read_b64_tr_b16), so no transpose pass;
+//   block j+1's DMA is in flight while block j computes (K and V
+//   double-buffered, one CTA barrier per block);
 //   within a block, the next MFMA operand fragments are read from LDS while
 //   the current ones feed the MFMAs.
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_f16 (A = 16 keys x 32 dims of K from
@@ -38,6 +40,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
 
 constexpr int kHD = 256;
 constexpr int kWaves = 8;
@@ -48,11 +52,8 @@ constexpr int kNDMA = 2048 / (64 * kWaves); // 16-byte DMA chunks per lane per K
 constexpr int kBM = kWaves * kRowsW;       // rows per CTA
 constexpr int kBN = 64;                    // keys per block
 constexpr int kKBytes = kBN * kHD * 2;     // K block, 32 KiB
-constexpr int kVTStride = (kBN + 4) * 2;   // V^T row (one dim) stride: 34 words, bank-spread
-constexpr int kVTBytes = kHD * kVTStride;  // 36 KiB
-constexpr int kVRaw = kBN * kHD * 2;      // raw V block staging (DMA target), 32 KiB
-// LDS: two K stages, one V^T buffer, one raw V buffer
-constexpr int kLdsBytes = 2 * kKBytes + kVTBytes + kVRaw;
+// LDS: two K stages then two V stages
+constexpr int kLdsBytes = 4 * kKBytes;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ _Float16 h16(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
@@ -200,86 +201,56 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
       }
     }
   };
-  // V: the raw block (64 rows x 512 B) arrives by DMA like K, chunk c of row r
-  // at slot c ^ ((r / 4) & 15) so the transpose's reads spread over the banks; then
-  // each thread transposes 4 keys x 8 dims (two such groups) into V^T [dim][key].
-  uint8_t *const vt = smem + 2 * kKBytes;
-  uint8_t *const vraw = vt + kVTBytes;
-  int v_goff[kNDMA];
-#pragma unroll
-  for (int r = 0; r < kNDMA; ++r) {
-    const int c = (w * kNDMA + r) * 64 + lane;
-    const int row = c >> 5;
-    v_goff[r] = row * (int)kvstride + 16 * ((c & 31) ^ ((row >> 2) & 15));
-  }
-  auto issue_v = [&](int blk) {
+  // V: same DMA and swizzle as K, into its own two stages.
+  auto issue_v = [&](int blk, int stage) {
+    uint8_t *vd = smem + (2 + stage) * kKBytes;
     const int j0 = blk * kBN;
     const uint8_t *src = vbase + (int64_t)j0 * kvstride;
     if (j0 + kBN - 1 <= kend) {
 #pragma unroll
       for (int r = 0; r < kNDMA; ++r)
-        __builtin_amdgcn_global_load_lds((const void *)(src + v_goff[r]),
-                                         (lds_void *)(vraw + (w * kNDMA + r) * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void *)(src + k_goff[r]),
+                                         (lds_void *)(vd + (w * kNDMA + r) * 1024), 16, 0, 0);
     } else {
 #pragma unroll
       for (int r = 0; r < kNDMA; ++r) {
         const int c = (w * kNDMA + r) * 64 + lane;
-        const int row = c >> 5;
-        const int jk = min(j0 + row, kend);
+        const int key = c >> 5, slot = c & 31;
+        const int jk = min(j0 + key, kend);
         __builtin_amdgcn_global_load_lds(
-            (const void *)(vbase + (int64_t)jk * kvstride + 16 * ((c & 31) ^ ((row >> 2) & 15))),
-                                         (lds_void *)(vraw + (w * kNDMA + r) * 1024), 16, 0, 0);
+            (const void *)(vbase + (int64_t)jk * kvstride + 16 * (slot ^ (key & 15))),
+            (lds_void *)(vd + (w * kNDMA + r) * 1024), 16, 0, 0);
       }
     }
   };
-  constexpr int kTG = 512 / kThreads;  // 4-key x 8-dim transpose groups per thread
-  int vr_off[kTG], vt_off[kTG];
-#pragma unroll
-  for (int gi = 0; gi < kTG; ++gi) {
-    const int u = tid + kThreads * gi;
-    const int kq = u & 15, c = u >> 4;  // key quad 0..15 (fastest), dim chunk 0..31
-    vr_off[gi] = 4 * kq * (kHD * 2) + 16 * (c ^ kq);  // raw V rows 4kq..4kq+3 hold chunk c at c ^ kq
-    vt_off[gi] = 8 * c * kVTStride + 8 * kq;
-  }
-  auto transpose_v = [&]() {
-#pragma unroll
-    for (int gi = 0; gi < kTG; ++gi) {
-      u32x4 x[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = *(const u32x4 *)(vraw + vr_off[gi] + i * (kHD * 2));
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {  // dim 8c + j: keys 4kq..4kq+3
-        const int wsel = j >> 1;
-        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
-        const uint32_t lo = __builtin_amdgcn_perm(x[1][wsel], x[0][wsel], sel);
-        const uint32_t hi = __builtin_amdgcn_perm(x[3][wsel], x[2][wsel], sel);
-        *(u32x2 *)(vt + vt_off[gi] + j * kVTStride) = u32x2{lo, hi};
-      }
-    }
-  };
+  // PV operand by transposing load: in each 16-lane group, source lane s points
+  // at key (base + s/4), dims 4(s%4)..+3 of a 16-dim tile; lane r then receives
+  // dim r of those 4 keys. Key bits 0-3 select the swizzle (base is a multiple
+  // of 16 apart from the lane group's 4g), so the per-lane part is fixed.
+  const int tr_kx = 4 * g + (n >> 2);                       // key & 15 of this source lane
+  const int tr_off = tr_kx * (kHD * 2) + 8 * (n & 1);        // row and 8-byte half
+  const int tr_m = 16 * ((n >> 1 & 1) ^ tr_kx);             // swizzle term of the chunk
   // LDS read offsets of the MFMA operands (block-invariant).
   // K: key 16kt + n, dims 32b + 8g: slot (4b + g) ^ n = 4(b ^ (n>>2)) + (g ^ (n&3)).
   int k_loff[8];
 #pragma unroll
   for (int b = 0; b < 8; ++b) k_loff[b] = n * (kHD * 2) + 64 * (b ^ (n >> 2)) + 16 * (g ^ (n & 3));
-  const int v_loff = n * kVTStride + 8 * g;  // V^T: dim 16dt + n, keys 32kg + 4g
 
   if (n_blocks > 0) {
     issue_k(0, 0);
-    issue_v(0);
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    transpose_v();
+    issue_v(0, 0);
   }
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int st = blk & 1;
     const bool more = blk + 1 < n_blocks;
-    __syncthreads();  // K stage st and V^T of block blk are complete; vraw is free
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA for blk landed
+    __syncthreads();  // every wave's DMA for blk landed; every wave is done with blk - 1
     if (more) {
       issue_k(blk + 1, st ^ 1);
-      issue_v(blk + 1);
+      issue_v(blk + 1, st ^ 1);
     }
     const uint8_t *kd = smem + st * kKBytes;
+    const uint8_t *vd = smem + (2 + st) * kKBytes;
     const int j0 = blk * kBN;
     const bool need_mask = (j0 + kBN - 1) > wave_min_lim;
 
@@ -357,18 +328,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 #pragma unroll
         for (int i = 0; i < 8; ++i) pf[sl][kg][i] = (_Float16)s[sl][2 * kg + (i >> 2)][i & 3];
     }
-    // ---- O^T += V^T P^T: A = 16 dims x 32 keys of V^T (shared by both slabs);
-    // fragments for the next 4 dim tiles are read while the current 4 run.
+    // ---- O^T += V^T P^T: A = 16 dims x 32 keys of V (k-slot 8g + j is key
+    // 32kg + 16(j/4) + 4g + j%4, as in pf), two transposing loads per operand;
+    // the next two dim tiles' operands are read while the current ones run.
 #pragma unroll
     for (int kg = 0; kg < 2; ++kg) {
-      u32x4 vb[2][2];
+      half8 vb[2][2];
       auto read_vb = [&](int buf, int dt0) {
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
-          const uint8_t *vrow = vt + 16 * (dt0 + d) * kVTStride + 64 * kg + v_loff;
-          const u32x2 lo = *(const u32x2 *)vrow;         // keys 32kg + 4g .. +3
-          const u32x2 hi = *(const u32x2 *)(vrow + 32);  // keys 32kg + 16 + 4g .. +3
-          vb[buf][d] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          const uint8_t *a0 = vd + (32 * kg) * (kHD * 2) + tr_off + ((32 * (dt0 + d)) ^ tr_m);
+          const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4 *)a0);
+          const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4 *)(a0 + 16 * (kHD * 2)));
+          vb[buf][d] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
       };
       read_vb(0, 0);
@@ -378,17 +350,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
           const int dt = 2 * q2 + d;
-          const half8 vf = __builtin_bit_cast(half8, vb[q2 & 1][d]);
 #pragma unroll
           for (int sl = 0; sl < kNSL; ++sl)
-            o[sl][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[sl][kg], o[sl][dt], 0, 0, 0);
+            o[sl][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb[q2 & 1][d], pf[sl][kg], o[sl][dt], 0, 0, 0);
         }
       }
-    }
-    if (more) {
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA for blk+1 landed
-      __syncthreads();  // every wave is done reading V^T of blk; all DMA landed
-      transpose_v();
     }
   }
 

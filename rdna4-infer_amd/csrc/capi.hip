@@ -46,7 +46,8 @@ constexpr int kMaxDevices = 64;
 constexpr int64_t kPartialFloats = 16ll << 20;  // 64 MiB
 constexpr int64_t kCounterWords = 1 << 20;
 struct Scratch {
-  float *partial = nullptr;
+  float *partial = nullptr;    // uncached: records exchanged between CTAs inside a launch
+  float *partial_c = nullptr;  // cached: records handed to a later launch
   unsigned *counters = nullptr;
 };
 Scratch g_scratch[kMaxDevices];
@@ -64,7 +65,8 @@ int get_scratch(Scratch **out) {
     if (hipExtMallocWithFlags((void **)&s.partial, kPartialFloats * sizeof(float),
                               hipDeviceMallocUncached) != hipSuccess)
       return fail(RD4_ENOMEM, "scratch allocation failed%s");
-    if (hipMalloc(&s.counters, kCounterWords * sizeof(unsigned)) != hipSuccess ||
+    if (hipMalloc(&s.partial_c, kPartialFloats * sizeof(float)) != hipSuccess ||
+        hipMalloc(&s.counters, kCounterWords * sizeof(unsigned)) != hipSuccess ||
         hipMemset(s.counters, 0, kCounterWords * sizeof(unsigned)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
       return fail(RD4_ENOMEM, "counter allocation failed%s");
@@ -113,7 +115,7 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   const bool mfma = aligned16 && decode_mfma_supported(kt, vt, n_head, n_head_kv, head_dim);
   if (splits <= 0) {  // automatic, at least -splits
     const int min_s = -splits;
-    splits = mfma ? auto_splits(t + 1, n_head_kv * n_chunks, 256, 128)
+    splits = mfma ? auto_splits(t + 1, n_head_kv * n_chunks, 256, 64)
                   : auto_splits(t + 1, n_head_kv * n_chunks, 1024, 64);
     if (splits < min_s) splits = min_s;
   }
@@ -144,7 +146,9 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
     while (splits > 1 && floats_for(splits) > kPartialFloats) splits = (splits + 1) / 2;
     const int64_t ctr_words = (int64_t)n_tok * n_head_kv * n_chunks * kCtrStride;
     if (ctr_words > kCounterWords) splits = 1;
-    a.partial = s->partial;
+    // The MFMA decode merges its records in a second launch (cached scratch
+    // suffices); the in-kernel merge tree needs the uncached one.
+    a.partial = (mfma && decode_mfma_ext_merge()) ? s->partial_c : s->partial;
     a.counters = s->counters;
     const int64_t rows = (int64_t)n_tok * n_head;
     const int NG = (splits + kMergeFan - 1) / kMergeFan;
