@@ -71,6 +71,24 @@ double rd4_kv_bytes_per_elem(int type);
 /* kv_row_bytes (kv.h:155): bytes of one head_dim row; -1 outside the enum. */
 int64_t rd4_kv_row_bytes(int type, int head_dim);
 
+/* ---- KV budget (device.h:36-50, 148-190) ----------------------------------- */
+
+/* kv_cache_bytes (device.h:176): bytes of the K and V caches of the reference
+ * model shape (16 full-attention layers x 4 kv heads x head_dim 256) at
+ * ctx_size tokens, computed exactly as the reference does (a double product,
+ * truncated). 0 for a type outside the enum. */
+uint64_t rd4_kv_cache_bytes(uint64_t ctx_size, int kt, int vt);
+/* The same for any attention shape: n_layers x n_head_kv rows of head_dim
+ * elements per token for K and for V. 0 for a bad type or shape. */
+uint64_t rd4_kv_cache_bytes_shape(uint64_t ctx_size, int n_layers, int n_head_kv, int head_dim,
+                                  int kt, int vt);
+/* Largest context whose caches fit in budget_bytes after reserved_bytes (the
+ * weights, buffers and the reference's allocator margin), capped at the
+ * reference's kMaxCtxSize (2^24, device.h:167). 0 when nothing fits or the
+ * arguments are invalid. Sized for a whole GPU: MI355X has 288 GB of HBM. */
+uint64_t rd4_kv_max_ctx(uint64_t budget_bytes, uint64_t reserved_bytes, int n_layers, int n_head_kv,
+                        int head_dim, int kt, int vt);
+
 /* ---- KV append / fill / dequant (kv.h:386-694) --------------------------- */
 
 /* kv_store_row_launch (kv.h:683): quantize `width` contiguous f32 values into

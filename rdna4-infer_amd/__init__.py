@@ -19,6 +19,9 @@ OK, EINVAL, ETYPE, ELAUNCH, ENOMEM = 0, -1, -2, -3, -4
 # exported symbol -> (argtypes, restype); the C-ABI test checks include/ against this
 _P, _I, _I64, _F, _U32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_uint32
 SIGNATURES = {
+    "rd4_kv_cache_bytes": ([ctypes.c_uint64, ctypes.c_int, ctypes.c_int], ctypes.c_uint64),
+    "rd4_kv_cache_bytes_shape": ([ctypes.c_uint64] + [ctypes.c_int] * 5, ctypes.c_uint64),
+    "rd4_kv_max_ctx": ([ctypes.c_uint64, ctypes.c_uint64] + [ctypes.c_int] * 5, ctypes.c_uint64),
     "rd4_version": ([], ctypes.c_char_p),
     "rd4_init": ([], _I),
     "rd4_last_error": ([], ctypes.c_char_p),
@@ -200,3 +203,16 @@ def sigmoid_gate(g, y):
 def rope(x, n_tokens, n_heads, head_dim, n_rot, freq_base, pos):
     _check(lib().rd4_rope_launch(_ptr(x), n_tokens, n_heads, head_dim, n_rot, freq_base, _ptr(pos),
                                  _stream()), "rope")
+
+
+def kv_cache_bytes(ctx_size, kt, vt, n_layers=None, n_head_kv=None, head_dim=None):
+    """KV cache bytes at ctx_size tokens (device.h:176): the reference model
+    shape by default, or n_layers x n_head_kv x head_dim per side."""
+    if n_layers is None:
+        return lib().rd4_kv_cache_bytes(ctx_size, kt, vt)
+    return lib().rd4_kv_cache_bytes_shape(ctx_size, n_layers, n_head_kv, head_dim, kt, vt)
+
+
+def kv_max_ctx(budget_bytes, reserved_bytes, n_layers, n_head_kv, head_dim, kt, vt):
+    """Largest context whose KV caches fit in budget_bytes - reserved_bytes."""
+    return lib().rd4_kv_max_ctx(budget_bytes, reserved_bytes, n_layers, n_head_kv, head_dim, kt, vt)

@@ -178,6 +178,39 @@ int rd4_init(void) {
 
 const char *rd4_last_error(void) { return g_err; }
 
+uint64_t rd4_kv_cache_bytes_shape(uint64_t ctx_size, int n_layers, int n_head_kv, int head_dim,
+                                  int kt, int vt) {
+  if (!valid_type(kt) || !valid_type(vt) || n_layers <= 0 || n_head_kv <= 0 || head_dim <= 0)
+    return 0;
+  // per token: n_layers * n_head_kv * head_dim elements on each side; the
+  // reference forms the product in double and truncates (device.h:176-179)
+  const double half = (double)n_layers * (double)n_head_kv * (double)head_dim;
+  return (uint64_t)((double)ctx_size * half * (rd4_kv_bytes_per_elem(kt) + rd4_kv_bytes_per_elem(vt)));
+}
+
+uint64_t rd4_kv_cache_bytes(uint64_t ctx_size, int kt, int vt) {
+  return rd4_kv_cache_bytes_shape(ctx_size, 16, 4, 256, kt, vt);
+}
+
+uint64_t rd4_kv_max_ctx(uint64_t budget_bytes, uint64_t reserved_bytes, int n_layers, int n_head_kv,
+                        int head_dim, int kt, int vt) {
+  constexpr uint64_t kMaxCtx = 1ull << 24;  // the reference's kMaxCtxSize
+  if (rd4_kv_cache_bytes_shape(1, n_layers, n_head_kv, head_dim, kt, vt) == 0 ||
+      reserved_bytes >= budget_bytes)
+    return 0;
+  const uint64_t avail = budget_bytes - reserved_bytes;
+  auto fits = [&](uint64_t c) {
+    return rd4_kv_cache_bytes_shape(c, n_layers, n_head_kv, head_dim, kt, vt) <= avail;
+  };
+  if (fits(kMaxCtx)) return kMaxCtx;
+  uint64_t lo = 0, hi = kMaxCtx;  // fits(lo), !fits(hi)
+  while (hi - lo > 1) {
+    const uint64_t mid = lo + (hi - lo) / 2;
+    (fits(mid) ? lo : hi) = mid;
+  }
+  return lo;
+}
+
 const char *rd4_kv_type_name(int type) {
   static const char *names[] = {"f32", "f16", "q8_0", "q4_0", "q5_0", "q4_1"};
   return valid_type(type) ? names[type] : "<unknown-kv-type>";

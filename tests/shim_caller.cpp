@@ -9,6 +9,7 @@
 #include "rdna4/attn.cuh"
 #include "rdna4/attn_fa2.cuh"
 #include "rdna4/attn_gate.h"
+#include "rdna4/kv_budget.h"
 
 using namespace rdna4;
 
@@ -56,6 +57,12 @@ int main() {
                            KvType::F16, KvType::F16, 1));
   CHECK(!attn_launch_split_wpb(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 24, 4, 256, 1.f,
                                KvType::F16, KvType::F16, 1, 12));
+  // device.h budget helpers (check_kvtype.hip:150-152 values)
+  CHECK(kv_cache_bytes(131072, KvType::F16, KvType::F16) == 8589934592ull);
+  CHECK(kv_cache_bytes(131072, "q8_0", "q8_0") == 4563402752ull);
+  CHECK(kv_cache_bytes(131072, "q9_9", "q8_0") == 0);
+  CHECK(required_bytes(1000, 0, KvType::F16, KvType::F16, 24) == 1024 + kOverheadBytes);
+  CHECK(max_ctx_size(288000000000ull, 20000000000ull, 0, KvType::Q4_0, KvType::Q4_0) > 0);
   std::printf(fails ? "FAILED %d\n" : "OK\n", fails);
   return fails ? 1 : 0;
 }
