@@ -188,6 +188,36 @@ int rd4_sigmoid_gate_launch(float *g_io, float *y_io, int64_t n, void *stream);
 int rd4_rope_launch(float *x, int n_tokens, int n_heads, int head_dim, int n_rot,
                     float freq_base, const int *pos, void *stream);
 
+/* ---- pre-attention epilogue (nn.cuh:24-63,239; graph.cuh:914-954) -------- */
+
+/* rms_norm_launch (nn.cuh:239): per row of ncols f32, y = x * scale * w with
+ * scale = rsqrtf(sum(x^2) / ncols + eps), the sum in the reference's order (256
+ * chained fmaf partials and a halving tree), so y is bit-identical to the
+ * reference kernel built for the same GPU. w may be NULL (no weight); y may be x. */
+int rd4_rms_norm_launch(const float *x, const float *w, float *y, int64_t nrows, int64_t ncols,
+                        float eps, void *stream);
+
+/* Fused pre-attention epilogue: for each of n_tok tokens, the six launches
+ * deinterleave_q_gate + rms_norm(q) + rms_norm(k) + rope(q) + rope(k) +
+ * kv_write_batch of graph.cuh:914-954 (one token) and graph.cuh:1444-1462 (a
+ * chunk) in one launch, with the same bits as that sequence:
+ *   qg      [n_tok][n_head][2][head_dim]  projection output, q then gate per head
+ *   k_new, v_new [n_tok][n_head_kv][head_dim]
+ *   q_norm, k_norm [head_dim] weights (NULL = none); eps as rms_norm
+ *   RoPE over the first n_rot dims (even, <= head_dim) at position pos[i]
+ *   q_out   [n_tok][n_head][head_dim]  normed, rotated q
+ *   gate_out (may be NULL)            the raw gate half, deinterleaved
+ *   k_out   (may be NULL, may be k_new) the normed, rotated k
+ *   K/V cache rows pos[i] * n_head_kv + h of k / v, quantized as kt / vt.
+ * The reference's kv_write_batch stores token i at row pos0 + i; here the row
+ * is pos[i], equal for the consecutive positions the graph passes. head_dim is
+ * 64, 128, 256 or 512; f32 buffers 16-byte aligned. */
+int rd4_qk_norm_rope_append(const float *qg, const float *k_new, const float *v_new,
+                            const float *q_norm, const float *k_norm, float eps, int n_rot,
+                            float freq_base, const int *pos, int n_tok, int n_head, int n_head_kv,
+                            int head_dim, float *q_out, float *gate_out, float *k_out, void *k,
+                            void *v, int kt, int vt, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

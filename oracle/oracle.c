@@ -17,6 +17,8 @@
  *                                    brute-force numpy softmax on small cases
  *   orc_merge                        equality with unsplit attention
  *   orc_sigmoid_gate                 closed form vs numpy
+ *   orc_rms_norm                     power-of-two rows (exact scale), f64 numpy
+ *                                    formula, the halving tree vs a plain sum
  */
 #include "oracle.h"
 
@@ -453,6 +455,29 @@ void orc_rope(float *x, int n_tokens, int n_heads, int head_dim, int n_rot, floa
         b[p + pairs] = (float)(x0 * s + x1 * c);
       }
     }
+}
+
+void orc_rms_norm(const float *x, const float *w, float *y, int64_t nrows, int64_t ncols,
+                  float eps) {
+  enum { T = 256 };
+  for (int64_t r = 0; r < nrows; ++r) {
+    const float *xr = x + r * ncols;
+    float *yr = y + r * ncols;
+    float part[T];
+    for (int t = 0; t < T; ++t) {
+      float acc = 0.0f;
+      for (int64_t i = t; i < ncols; i += T) acc = fmaf(xr[i], xr[i], acc);
+      part[t] = acc;
+    }
+    for (int s = T / 2; s > 0; s >>= 1)
+      for (int t = 0; t < s; ++t) part[t] = part[t] + part[t + s];
+    const float mean = part[0] / (float)ncols + eps;
+    const float scale = (float)(1.0 / sqrt((double)mean));
+    for (int64_t i = 0; i < ncols; ++i) {
+      const float v = xr[i] * scale;
+      yr[i] = w ? v * w[i] : v;
+    }
+  }
 }
 
 /* ------------------------------------------------------------- inputs --- */

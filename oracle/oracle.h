@@ -64,6 +64,13 @@ void orc_sigmoid_gate(float *g, float *y, int64_t n);
 void orc_rope(float *x, int n_tokens, int n_heads, int head_dim, int n_rot, float freq_base,
               const int *pos);
 
+/* Row RMSNorm in rms_norm_kernel's f32 order (nn.cuh:24-63): 256 chained fmaf
+ * partials over elements t, t+256, ..., a halving tree p[t] += p[t+s], then
+ * y = (x * scale) * w with scale = 1/sqrt(sum/ncols + eps) correctly rounded
+ * (the device rsqrtf is within 1 ulp of it). w may be NULL. */
+void orc_rms_norm(const float *x, const float *w, float *y, int64_t nrows, int64_t ncols,
+                  float eps);
+
 /* Seeded N(0,1) generator used by every test and bench input (splitmix64 +
  * Box-Muller). Deterministic across platforms. */
 void orc_randn(float *dst, int64_t n, uint64_t seed);

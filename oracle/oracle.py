@@ -59,6 +59,8 @@ def lib():
         L.orc_sigmoid_gate.restype = None
         L.orc_rope.argtypes = [P, I, I, I, I, F, P]
         L.orc_rope.restype = None
+        L.orc_rms_norm.argtypes = [P, P, P, I64, I64, F]
+        L.orc_rms_norm.restype = None
         L.orc_randn.argtypes = [P, I64, ctypes.c_uint64]
         L.orc_randn.restype = None
         _lib = L
@@ -153,6 +155,18 @@ def rope(x, n_tokens, n_heads, head_dim, n_rot, freq_base, pos):
     pos = np.ascontiguousarray(pos, np.int32)
     lib().orc_rope(_p(x), n_tokens, n_heads, head_dim, n_rot, freq_base, _p(pos))
     return x
+
+
+def rms_norm(x, w, ncols, eps):
+    """Row RMSNorm in the reference's f32 order (nn.cuh:24-63); w may be None."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    wp = None
+    if w is not None:
+        w = np.ascontiguousarray(w, np.float32)
+        wp = _p(w)
+    lib().orc_rms_norm(_p(x), wp, _p(y), x.size // ncols, ncols, eps)
+    return y
 
 
 def ref_lib():

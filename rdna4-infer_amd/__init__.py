@@ -46,6 +46,9 @@ SIGNATURES = {
     "rd4_prefill": ([_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I),
     "rd4_sigmoid_gate_launch": ([_P, _P, _I64, _P], _I),
     "rd4_rope_launch": ([_P, _I, _I, _I, _I, _F, _P, _P], _I),
+    "rd4_rms_norm_launch": ([_P, _P, _P, _I64, _I64, _F, _P], _I),
+    "rd4_qk_norm_rope_append": ([_P, _P, _P, _P, _P, _F, _I, _F, _P, _I, _I, _I, _I, _P, _P, _P,
+                                 _P, _P, _I, _I, _P], _I),
 }
 
 _lib = None
@@ -203,6 +206,23 @@ def sigmoid_gate(g, y):
 def rope(x, n_tokens, n_heads, head_dim, n_rot, freq_base, pos):
     _check(lib().rd4_rope_launch(_ptr(x), n_tokens, n_heads, head_dim, n_rot, freq_base, _ptr(pos),
                                  _stream()), "rope")
+
+
+def rms_norm(x, w, y, nrows, ncols, eps):
+    """rms_norm_launch (nn.cuh:239): y <- x * rsqrt(mean(x^2) + eps) * w per row."""
+    _check(lib().rd4_rms_norm_launch(_ptr(x), _ptr(w), _ptr(y), nrows, ncols, eps, _stream()),
+           "rms_norm")
+
+
+def qk_norm_rope_append(qg, k_new, v_new, q_norm, k_norm, eps, n_rot, freq_base, pos, n_tok,
+                        n_head, n_head_kv, head_dim, q_out, k_cache, v_cache, kt, vt,
+                        gate_out=None, k_out=None):
+    """Fused deinterleave + q/k RMSNorm + RoPE + K/V cache append
+    (graph.cuh:914-954): one launch for the six of the reference."""
+    _check(lib().rd4_qk_norm_rope_append(
+        _ptr(qg), _ptr(k_new), _ptr(v_new), _ptr(q_norm), _ptr(k_norm), eps, n_rot, freq_base,
+        _ptr(pos), n_tok, n_head, n_head_kv, head_dim, _ptr(q_out), _ptr(gate_out), _ptr(k_out),
+        _ptr(k_cache), _ptr(v_cache), kt, vt, _stream()), "qk_norm_rope_append")
 
 
 def kv_cache_bytes(ctx_size, kt, vt, n_layers=None, n_head_kv=None, head_dim=None):

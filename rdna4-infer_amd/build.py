@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librdna4attn.so")
-SOURCES = ["kv.hip", "attn_generic.hip", "attn_decode_mfma.hip", "attn_prefill_mfma.hip", "prefill.hip", "misc.hip", "merge.hip", "capi.hip"]
+SOURCES = ["kv.hip", "attn_generic.hip", "attn_decode_mfma.hip", "attn_prefill_mfma.hip", "prefill.hip", "misc.hip", "merge.hip", "qk_epilogue.hip", "capi.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",

@@ -19,6 +19,13 @@ hipError_t kv_load_launch(int t, const uint8_t *src, float *dst, int64_t n, hipS
 hipError_t sigmoid_gate_launch(float *g, float *y, int64_t n, hipStream_t st);
 hipError_t rope_launch(float *x, int n_tokens, int n_heads, int head_dim, int n_rot,
                        float freq_base, const int *pos, hipStream_t st);
+hipError_t rms_norm_launch(const float *x, const float *w, float *y, int64_t nrows, int64_t ncols,
+                           float eps, hipStream_t st);
+hipError_t qk_epilogue_launch(const float *qg, const float *k, const float *v, const float *qw,
+                              const float *kw, float eps, int n_rot, float freq_base,
+                              const int *pos, int n_tok, int n_head, int n_head_kv, int head_dim,
+                              float *q_out, float *gate_out, float *k_out, uint8_t *kc,
+                              uint8_t *vc, int kt, int vt, hipStream_t st);
 }  // namespace rd4
 
 using namespace rd4;
@@ -412,6 +419,37 @@ int rd4_rope_launch(float *x, int n_tokens, int n_heads, int head_dim, int n_rot
   return launched(
       rope_launch(x, n_tokens, n_heads, head_dim, n_rot, freq_base, pos, (hipStream_t)stream),
       "rope");
+}
+
+int rd4_rms_norm_launch(const float *x, const float *w, float *y, int64_t nrows, int64_t ncols,
+                        float eps, void *stream) {
+  if (nrows < 0 || ncols < 0 || nrows > 0x7fffffff || (nrows > 0 && ncols > 0 && (!x || !y)))
+    return fail(RD4_EINVAL, "bad rms_norm shape%s");
+  return launched(rms_norm_launch(x, w, y, nrows, ncols, eps, (hipStream_t)stream), "rms_norm");
+}
+
+int rd4_qk_norm_rope_append(const float *qg, const float *k_new, const float *v_new,
+                            const float *q_norm, const float *k_norm, float eps, int n_rot,
+                            float freq_base, const int *pos, int n_tok, int n_head, int n_head_kv,
+                            int head_dim, float *q_out, float *gate_out, float *k_out, void *k,
+                            void *v, int kt, int vt, void *stream) {
+  if (!valid_type(kt) || !valid_type(vt)) return fail(RD4_ETYPE, "KvType outside the enum%s");
+  if (n_tok < 0 || n_head < 1 || n_head_kv < 1 || n_head % n_head_kv != 0 ||
+      (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512) || n_rot < 0 ||
+      n_rot > head_dim || (n_rot & 1))
+    return fail(RD4_EINVAL, "bad epilogue shape%s");
+  if (n_tok == 0) return RD4_OK;
+  if (!qg || !k_new || !v_new || !pos || !q_out || !k || !v)
+    return fail(RD4_EINVAL, "epilogue buffer is NULL%s");
+  const void *f32s[] = {qg, k_new, v_new, q_out, gate_out, k_out};
+  for (const void *p : f32s)
+    if (((uintptr_t)p & 15) != 0) return fail(RD4_EINVAL, "epilogue f32 buffer not 16-byte aligned%s");
+  if (((uintptr_t)k & 3) || ((uintptr_t)v & 3))
+    return fail(RD4_EINVAL, "KV cache not 4-byte aligned%s");
+  return launched(qk_epilogue_launch(qg, k_new, v_new, q_norm, k_norm, eps, n_rot, freq_base, pos,
+                                     n_tok, n_head, n_head_kv, head_dim, q_out, gate_out, k_out,
+                                     (uint8_t *)k, (uint8_t *)v, kt, vt, (hipStream_t)stream),
+                  "qk epilogue");
 }
 
 }  // extern "C"

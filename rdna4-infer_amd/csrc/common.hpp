@@ -121,6 +121,23 @@ __device__ __forceinline__ void load4(const uint8_t *row, int64_t e, float out[4
   }
 }
 
+// Split-half RoPE of one pair (attn.cuh:36-46): the angle pos * base^(-2p/n_rot)
+// is formed in f32, and every product and sum rounds on its own (no FMA
+// contraction), so the standalone rope kernel and the fused epilogue give the
+// same bits.
+__device__ __forceinline__ void rope_cs(int pos, int p, int n_rot, float freq_base, float *c,
+                                        float *s) {
+  const float theta = (float)pos * powf(freq_base, -2.0f * (float)p / (float)n_rot);
+  *c = cosf(theta);
+  *s = sinf(theta);
+}
+__device__ __forceinline__ float rope_lo(float x0, float x1, float c, float s) {
+  return __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+}
+__device__ __forceinline__ float rope_hi(float x0, float x1, float c, float s) {
+  return __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+}
+
 // Wave64 butterfly helpers (lane masks stay inside the 64-lane wavefront).
 __device__ __forceinline__ float xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 __device__ __forceinline__ uint32_t xor_u(uint32_t v, int m) {

@@ -42,12 +42,12 @@ __global__ __launch_bounds__(128) void rope_kernel(float *__restrict__ x, int n_
   const int p = (int)(idx % pairs);
   const int64_t th = idx / pairs;  // token * n_heads + head
   const int t = (int)(th / n_heads);
-  const float theta = (float)pos[t] * powf(freq_base, -2.0f * (float)p / (float)n_rot);
-  const float c = cosf(theta), s = sinf(theta);
+  float c, s;
+  rope_cs(pos[t], p, n_rot, freq_base, &c, &s);
   float *b = x + th * head_dim;
   const float x0 = b[p], x1 = b[p + pairs];
-  b[p] = x0 * c - x1 * s;
-  b[p + pairs] = x0 * s + x1 * c;
+  b[p] = rope_lo(x0, x1, c, s);
+  b[p + pairs] = rope_hi(x0, x1, c, s);
 }
 
 hipError_t sigmoid_gate_launch(float *g, float *y, int64_t n, hipStream_t st) {

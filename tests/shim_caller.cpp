@@ -24,6 +24,9 @@ static_assert(std::is_same_v<decltype(&fa2_prefill_launch),
                                       hipStream_t)>);
 static_assert(std::is_same_v<decltype(&sigmoid_gate_launch),
                              bool (*)(float *, float *, std::int64_t, hipStream_t)>);
+static_assert(std::is_same_v<decltype(&rms_norm_launch),
+                             bool (*)(const float *, const float *, float *, std::int64_t,
+                                      std::int64_t, float, hipStream_t)>);
 
 static int fails = 0;
 #define CHECK(c)                                              \

@@ -383,3 +383,44 @@ def test_golden_vectors(orc):
     got = orc.attn_batch(z["q"], z["k"], z["v"], z["pos"], meta["n_head"], meta["n_kv"],
                          meta["hd"], meta["scale"], meta["kt"], meta["vt"])
     assert np.abs(got - z["attn"]).max() <= 1e-6
+
+
+def test_rms_norm_power_of_two_rows_exact(orc):
+    # |x| = 2^k everywhere: mean(x^2) = 4^k and the scale 2^-k are exact, so y = sign(x) * w
+    for ncols, k in ((64, 3), (256, -2), (512, 5), (1000, 1)):
+        sign = np.where(orc.randn(ncols, ncols) > 0, 1.0, -1.0).astype(np.float32)
+        x = (sign * 2.0 ** k).astype(np.float32)
+        w = orc.randn(ncols, 7 + ncols)
+        assert np.array_equal(orc.rms_norm(x, w, ncols, 0.0), sign * w)
+        assert np.array_equal(orc.rms_norm(x, None, ncols, 0.0), sign)
+
+
+def test_rms_norm_tree_order(orc):
+    """One large element among ones, 5120 columns (nn.cuh:37-59): thread 0's fmaf chain
+    2^24 + 1 + ... rounds every +1 away, each other thread's chain sums 20 ones, and the
+    halving tree adds those 255 partials exactly: sum = 2^24 + 5100. A sequential sum
+    (2^24), a 128-partial tree (2^24 + 5080) or the exact sum (2^24 + 5119) give other
+    scales."""
+    n = 5120
+    x = np.ones(n, np.float32)
+    x[0] = 4096.0
+    y = orc.rms_norm(x, None, n, 0.0)
+
+    def scale_of(total):
+        mean = np.float32(np.float32(total) / np.float32(n))
+        return np.float32(1.0 / np.sqrt(np.float64(mean)))
+
+    want = scale_of(2.0 ** 24 + 5100)
+    assert y[1] == want and y[0] == np.float32(4096.0 * np.float64(want))
+    for other in (2.0 ** 24, 2.0 ** 24 + 5080, 2.0 ** 24 + 5119):
+        assert scale_of(other) != want
+
+
+def test_rms_norm_matches_f64(orc):
+    for rows, ncols, eps in ((24, 256, 1e-6), (3, 1000, 1e-5), (2, 5120, 1e-6), (4, 64, 0.1)):
+        x = orc.randn(rows * ncols, rows + ncols).reshape(rows, ncols)
+        w = orc.randn(ncols, 3 * ncols)
+        got = orc.rms_norm(x, w, ncols, eps)
+        x64 = x.astype(np.float64)
+        want = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + eps) * w
+        assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
