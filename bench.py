@@ -82,12 +82,13 @@ def event_loop_ms(torch, fn, steps):
     return a.elapsed_time(b) / steps
 
 
-def decode_workload(torch, rd4, kt, ctx, outlier, gated=True):
+def decode_workload(torch, rd4, kt, ctx, outlier, gated=True, vt=None):
     """Returns (step_fn(timer), algorithmic step bytes, dominant-kernel bytes, cpu_fn, info)."""
+    vt = kt if vt is None else vt
     pos = ctx - 1
-    rb = rd4.kv_row_bytes(kt, HD)
+    krb, vrb = rd4.kv_row_bytes(kt, HD), rd4.kv_row_bytes(vt, HD)
     kc = make_cache(torch, rd4, kt, ctx, SEED, outlier)
-    vc = make_cache(torch, rd4, kt, ctx, SEED + 1, outlier)
+    vc = make_cache(torch, rd4, vt, ctx, SEED + 1, outlier)
     g = torch.Generator(device="cuda").manual_seed(SEED + 2)
     q = torch.randn(NH * HD, generator=g, device="cuda")
     gate0 = torch.randn(NH * HD, generator=g, device="cuda")
@@ -99,12 +100,12 @@ def decode_workload(torch, rd4, kt, ctx, outlier, gated=True):
 
     def step():
         # one launch: quantize-append the token's K/V rows at `pos`, gated attention over 0..pos
-        rd4.attn_decode_append(q, krow, vrow, kc, vc, out, pos, NH, NKV, HD, scale, kt, kt,
+        rd4.attn_decode_append(q, krow, vrow, kc, vc, out, pos, NH, NKV, HD, scale, kt, vt,
                                gate=gate if gated else None)
 
-    kv_bytes = ctx * NKV * 2 * rb
+    kv_bytes = ctx * NKV * (krb + vrb)
     small = NH * HD * 4 * (4 if gated else 2)  # q, out (+ gate read and write)
-    append = 2 * NKV * HD * 4 + 2 * NKV * rb
+    append = 2 * NKV * HD * 4 + NKV * (krb + vrb)
     attn_bytes = kv_bytes + small + append  # the append is inside the attention launch
     step_bytes = attn_bytes
 
@@ -116,14 +117,15 @@ def decode_workload(torch, rd4, kt, ctx, outlier, gated=True):
         qh = q.cpu().numpy()
         reps, t0 = 0, time.perf_counter()
         while True:
-            orc.attn_decode(qh, kh, vh, pos, NH, NKV, HD, scale, kt, kt)
+            orc.attn_decode(qh, kh, vh, pos, NH, NKV, HD, scale, kt, vt)
             reps += 1
             if time.perf_counter() - t0 > budget_s:
                 break
         dt = (time.perf_counter() - t0) / reps
         return attn_bytes / dt / 1e9, "full decode step over %d keys x %d reps" % (ctx, reps)
 
-    info = {"workload": "decode", "kv_type": rd4.TYPE_NAMES[kt], "ctx": ctx, "n_head": NH,
+    kv_name = rd4.TYPE_NAMES[kt] if kt == vt else rd4.TYPE_NAMES[kt] + "/" + rd4.TYPE_NAMES[vt]
+    info = {"workload": "decode", "kv_type": kv_name, "ctx": ctx, "n_head": NH,
             "n_head_kv": NKV, "head_dim": HD, "gate": gated, "append": True, "seed": SEED}
     return step, step, step_bytes, attn_bytes, cpu, info
 
@@ -200,7 +202,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode_q8_0",
-                    choices=["decode_q8_0", "decode_f16", "decode_q4_0", "prefill", "copy"])
+                    choices=["decode_q8_0", "decode_f16", "decode_q4_0", "decode_q5_0_q4_1",
+                             "prefill", "copy"])
     ap.add_argument("--extra", action="store_true", help="also measure the other configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
@@ -231,6 +234,8 @@ def main():
             return decode_workload(torch, rd4, 1, 32768, False)
         if name == "decode_q4_0":
             return decode_workload(torch, rd4, 3, 131001, False)
+        if name == "decode_q5_0_q4_1":  # the reference's 131K default pair
+            return decode_workload(torch, rd4, 4, 131001, False, vt=5)
         return prefill_workload(torch, rd4)
 
     step, dom, step_units, dom_units, cpu, info = build(args.workload)
@@ -268,7 +273,7 @@ def main():
                                "host_nproc": os.cpu_count()}
     if args.extra:
         res["extra"] = {}
-        for name in ("decode_f16", "decode_q4_0", "prefill"):
+        for name in ("decode_f16", "decode_q4_0", "decode_q5_0_q4_1", "prefill"):
             if name == args.workload:
                 continue
             st, dm, su, du, _, inf = build(name)

@@ -1,4 +1,5 @@
-// Split-KV GQA decode on f16 MFMA (gfx950), K/V in f16, q8_0 or q4_0.
+// Split-KV GQA decode on f16 MFMA (gfx950). K in f16, q8_0, q4_0, q5_0 or
+// q4_1; V in f16, q8_0, q4_0 or q4_1.
 //
 // Reference semantics: attn_split_kernel + attn_merge_kernel and the batched
 // forms (include/rdna4/attn.cuh:445-590, 686-845) with the output gate of
@@ -13,17 +14,19 @@
 //      16-byte global loads issued one tile ahead into registers, and are
 //      written to a wave-private LDS buffer;
 //   2. S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K
-//      converted to f16 on the fly (f16 as is; q8_0/q4_0 integers, exact in
-//      f16), B = the query rows. The 16 MFMA rows carry the group's query heads
-//      twice, as f16 hi and lo parts (q = hi + lo to 2^-22), so the f32 query
-//      costs no precision. Quantized K is scaled by its per-(key, block) d after
-//      each 32-dim block's MFMA;
+//      converted to f16 on the fly (f16 as is; the quantized types' integers,
+//      exact in f16), B = the query rows. The 16 MFMA rows carry the group's
+//      query heads twice, as f16 hi and lo parts (q = hi + lo to 2^-22), so the
+//      f32 query costs no precision. Quantized K is scaled by its per-(key,
+//      block) d after each 32-dim block's MFMA; q4_1's offset m adds
+//      m * sum(q over the block), the block sums formed once per CTA;
 //   3. online softmax in registers (exp2 domain); the C layout of S^T gives each
 //      lane one query row x 4 keys, exactly the B operand layout PV needs; the
 //      O rescale is skipped when no row's running max moved;
 //   4. O^T += V^T P^T on v_mfma_f32_16x16x16_f16: A = 16 dims x 16 keys of V
 //      read from LDS, B = p (hi/lo rows again), with the quantized V's d folded
-//      into p per 32-dim block.
+//      into p per 32-dim block; q4_1's offsets contribute sum_j p_j m_j per
+//      block, kept in f32 registers and added to the block's dims at the end.
 // The 4 waves' states merge through LDS into one (m, l, acc) record per query
 // head; splits merge through the two-level tree of merge.hpp in the same launch.
 #include <cstdlib>
@@ -90,8 +93,10 @@ struct TileShape {
   static constexpr int KCH = kTile * KC, VCH = kTile * VC;
   static constexpr int NI = (KCH + VCH + 63) / 64;  // load instructions per tile
   static constexpr int TB = (KCH + VCH) * 16;       // bytes per ring stage
-  // per-wave f32 scale tables [block][key] for the quantized K and V of a tile
-  static constexpr int DT = (KT != F16 ? 512 : 0) + (VT != F16 ? 512 : 0);
+  // per-wave f32 tables [block][key] of a tile, in this order: K scales, V
+  // scales (quantized types), K offsets, V offsets (q4_1)
+  static constexpr int NTK = (KT != F16) + (KT == Q4_1), NTV = (VT != F16) + (VT == Q4_1);
+  static constexpr int DT = 512 * (NTK + NTV);
 #ifndef RD4_DEC_WAVES_SMALL
 #define RD4_DEC_WAVES_SMALL 8
 #endif
@@ -138,6 +143,9 @@ __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const u
 // with j even are always two consecutive dims starting at an even dim.
 template <int KT>
 __host__ __device__ constexpr int k_dim(int b, int g, int j) {
+  // q5_0 / q4_1: low nibbles (g < 2) hold elements 0..15, high nibbles 16..31,
+  // read with aligned words (q4_1) or realigned words (q5_0) in every block
+  if (KT == Q5_0 || KT == Q4_1) return 32 * b + 16 * (g >> 1) + 8 * (g & 1) + j;
   if (KT == F16 || (b & 1)) {
     if (KT == Q4_0) return 32 * b + 16 * (g >> 1) + 8 * (g & 1) + j;
     return 32 * b + 8 * g + j;
@@ -168,6 +176,24 @@ __device__ __forceinline__ uint32_t nibpair_to_h2(uint32_t v, uint32_t sel) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w) + c);
 }
 
+// Low nibbles of the two bytes sel picks -> two f16 of the unsigned nibble (q4_1).
+__device__ __forceinline__ uint32_t unibpair_to_h2(uint32_t v, uint32_t sel) {
+  const uint32_t w = (__builtin_amdgcn_perm(0u, v, sel) & 0x000f000fu) | 0x64006400u;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 c = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w) + c);
+}
+// q5_0: low nibbles of the two bytes sel picks plus high bits hb0, hb1 (0/1)
+// -> two f16 of (nibble | hb << 4) - 16.
+__device__ __forceinline__ uint32_t q5pair_to_h2(uint32_t v, uint32_t sel, uint32_t hb0,
+                                                 uint32_t hb1) {
+  const uint32_t w = (__builtin_amdgcn_perm(0u, v, sel) & 0x000f000fu) | (hb0 << 4) |
+                     (hb1 << 20) | 0x64006400u;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 c = {(_Float16)-1040.0f, (_Float16)-1040.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w) + c);
+}
+
 // A operand of S^T = K Q^T for block b: lane (key = l%16, g = l/16) gets the
 // 8 dims k_dim<KT>(b, g, 0..7) of its key as f16. sel_edge is the per-lane
 // v_perm selector that gathers the edge bytes in the unaligned blocks
@@ -178,6 +204,40 @@ __device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g, int n
   u32x4 r;
   if constexpr (KT == F16) {
     r = *(const u32x4 *)(krow + 16 * ((4 * b + g) ^ n_of_row));
+  } else if constexpr (KT == Q4_1 || KT == Q5_0) {
+    constexpr int BB = block_bytes(KT);
+    const int gg = g & 1, sh = (g & 2) ? 4 : 0;
+    uint32_t x, y;
+    if constexpr (KT == Q4_1) {  // 20-byte blocks: qs at +4 is word aligned
+      x = lds_u32(krow + BB * b + 4 + 8 * gg);
+      y = lds_u32(krow + BB * b + 8 + 8 * gg);
+    } else if (b & 1) {  // 22-byte blocks: qs at +6 is word aligned in odd blocks
+      x = lds_u32(krow + BB * b + 6 + 8 * gg);
+      y = lds_u32(krow + BB * b + 10 + 8 * gg);
+    } else {
+      const uint32_t a0 = lds_u32(krow + BB * b + 4 + 8 * gg);
+      const uint32_t a1 = lds_u32(krow + BB * b + 8 + 8 * gg);
+      const uint32_t a2 = lds_u32(krow + BB * b + 12 + 8 * gg);
+      x = __builtin_amdgcn_alignbyte(a1, a0, 2);
+      y = __builtin_amdgcn_alignbyte(a2, a1, 2);
+    }
+    x >>= sh;
+    y >>= sh;
+    if constexpr (KT == Q4_1) {
+      r[0] = unibpair_to_h2(x, 0x0c010c00u);
+      r[1] = unibpair_to_h2(x, 0x0c030c02u);
+      r[2] = unibpair_to_h2(y, 0x0c010c00u);
+      r[3] = unibpair_to_h2(y, 0x0c030c02u);
+    } else {
+      // the block's 32 high bits at +2; this lane's 8 elements are bits
+      // 16 * (g >> 1) + 8 * gg ..
+      const uint32_t qh = lds_u16(krow + BB * b + 2) | (lds_u16(krow + BB * b + 4) << 16);
+      const uint32_t hb = qh >> (16 * (g >> 1) + 8 * gg);
+      r[0] = q5pair_to_h2(x, 0x0c010c00u, hb & 1u, (hb >> 1) & 1u);
+      r[1] = q5pair_to_h2(x, 0x0c030c02u, (hb >> 2) & 1u, (hb >> 3) & 1u);
+      r[2] = q5pair_to_h2(y, 0x0c010c00u, (hb >> 4) & 1u, (hb >> 5) & 1u);
+      r[3] = q5pair_to_h2(y, 0x0c030c02u, (hb >> 6) & 1u, (hb >> 7) & 1u);
+    }
   } else {
     constexpr int BB = block_bytes(KT);
     const int gg = KT == Q8_0 ? g : (g & 1);  // q4_0: lane groups g and g^2 read the same bytes
@@ -214,7 +274,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // operand lane with MFMA row r reads whole aligned words of its 4 keys:
 //   f16:  16-byte chunk r + 16h (dims 8(r + 16h) .. +7), one MFMA per dim, t = 8h + e;
 //   q8_0: the 2 bytes at dims 32b + 2r, +1 of block b, t = 2b + e;
-//   q4_0: byte r of block b (element r low nibble, r + 16 high), t = 2b + e;
+//   q4_0, q4_1: byte r of block b (element r low nibble, r + 16 high), t = 2b + e;
 // so every MFMA's rows lie in one quantization block and share one P' operand.
 template <int VT>
 __host__ __device__ constexpr int v_dim(int t, int r) {
@@ -226,6 +286,11 @@ __host__ __device__ constexpr int v_dim(int t, int r) {
 template <int T>
 __device__ __forceinline__ float scale_of(const uint8_t *row, int b) {
   return h2f((uint16_t)lds_u16(row + block_bytes(T) * b));
+}
+// q4_1's per-block offset m (the f16 after d)
+template <int T>
+__device__ __forceinline__ float offset_of(const uint8_t *row, int b) {
+  return h2f((uint16_t)lds_u16(row + block_bytes(T) * b + 2));
 }
 
 // hi/lo f16 pair of an f32 (x = hi + lo to ~2^-22 relative).
@@ -343,8 +408,15 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
 
   // ---- async tile ring: stage i of this wave at ring + (i % R) * TB
   uint8_t *ring = smem + w * (R * TB + DT);
-  float *dk_t = (float *)(ring + R * TB);                  // [8][16] K scales (quantized K)
-  float *dv_t = dk_t + (KT != F16 ? 128 : 0);              // [8][16] V scales (quantized V)
+  // tables [8 blocks][16 keys]: K scales, V scales, K offsets, V offsets
+  constexpr int iDK = KT != F16 ? 0 : -1;
+  constexpr int iDV = VT != F16 ? (KT != F16) : -1;
+  constexpr int iMK = KT == Q4_1 ? (KT != F16) + (VT != F16) : -1;
+  constexpr int iMV = VT == Q4_1 ? (KT != F16) + (VT != F16) + (KT == Q4_1) : -1;
+  float *dk_t = (float *)(ring + R * TB);
+  float *dv_t = dk_t + 128 * (iDV > 0 ? iDV : 0);
+  float *mk_t = dk_t + 128 * (iMK > 0 ? iMK : 0);
+  float *mv_t = dk_t + 128 * (iMV > 0 ? iMV : 0);
   const int n_tiles_all = (j_end - j_begin + kTile - 1) / kTile;
   const int my_tiles = (a.dbg & 32) ? 0 : (n_tiles_all > w ? (n_tiles_all - w + kWaves - 1) / kWaves : 0);
   // Global source of this lane's chunk in load instruction r of a tile:
@@ -446,14 +518,17 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   // once and the CTA exchanges them through LDS (over the query rows).
   const uint32_t lo_mask = n >= 8 ? 0xffffffffu : 0u;
   half8 qf[8];
+  float qblk[8];
   {
     const int hh = n & 7;
     const bool on = hh < G;
     const uint8_t *qrow = q_lds + (on ? hh : 0) * qsb;
     u32x4 mine[8 / kWaves];
+    float qsum_mine[8 / kWaves];  // q4_1 K: sum of the row's q over block b
 #pragma unroll
     for (int m = 0; m < 8 / kWaves; ++m) {
       const int b = w + kWaves * m;
+      float qs = 0.0f;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int d0 = k_dim<KT>(b, g, 2 * jj);
@@ -468,15 +543,29 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
           x1 = f.y;
         }
         mine[m][jj] = on ? split_prod2(x0, 1.0f, x1, 1.0f, lo_mask) : 0u;
+        if constexpr (KT == Q4_1) qs += x0 + x1;
       }
+      if constexpr (KT == Q4_1) {
+        qs += xor_f(qs, 16);
+        qs += xor_f(qs, 32);
+      }
+      qsum_mine[m] = qs;
     }
     __syncthreads();  // every wave has read the query rows
     u32x4 *qf_lds = (u32x4 *)q_lds;  // [block][lane]
+    float *qsum_lds = (float *)(q_lds + 8 * 64 * 16);  // [block][head]
 #pragma unroll
-    for (int m = 0; m < 8 / kWaves; ++m) qf_lds[(w + kWaves * m) * 64 + lane] = mine[m];
+    for (int m = 0; m < 8 / kWaves; ++m) {
+      qf_lds[(w + kWaves * m) * 64 + lane] = mine[m];
+      if (KT == Q4_1 && lane < 8) qsum_lds[(w + kWaves * m) * 8 + lane] = on ? qsum_mine[m] : 0.0f;
+    }
     __syncthreads();
 #pragma unroll
-    for (int b = 0; b < 8; ++b) qf[b] = __builtin_bit_cast(half8, qf_lds[b * 64 + lane]);
+    for (int b = 0; b < 8; ++b) {
+      qf[b] = __builtin_bit_cast(half8, qf_lds[b * 64 + lane]);
+      // the offset term goes to the hi rows only (rows n and n^8 are summed)
+      if constexpr (KT == Q4_1) qblk[b] = n < 8 ? qsum_lds[b * 8 + n] : 0.0f;
+    }
   }
   const float sl2 = a.scale * kLog2e;
   // edge gather of the unaligned quantized-K blocks: lane group 3 (q8_0) or
@@ -486,6 +575,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   floatx4 o[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float cm[8];  // q4_1 V: sum_j p_j m_j per block for this lane's row and keys
+#pragma unroll
+  for (int b = 0; b < 8; ++b) cm[b] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
   RD4_TP();
@@ -507,14 +599,17 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     RD4_TP();
     const uint8_t *kl = ring + (i % R) * TB;
     const uint8_t *vl = kl + KCH * 16;
-    if constexpr (DT > 0) {  // f16 scales of the tile -> f32 tables, once per tile
+    if constexpr (DT > 0) {  // f16 scales (and offsets) of the tile -> f32 tables, once per tile
 #pragma unroll
       for (int j = 0; j < DT / 256; ++j) {
         const int v = lane + 64 * j;
-        const bool isv = (KT == F16) || (VT != F16 && v >= 128);
-        const int vv = v & 127, key = vv & 15, b = vv >> 4;
-        const float d = isv ? scale_of<VT>(vl + key * VS, b) : scale_of<KT>(kl + key * KS, b);
-        (isv ? dv_t : dk_t)[b * 16 + key] = d;
+        const int ti = v >> 7, key = v & 15, b = (v >> 4) & 7;
+        float d;
+        if (ti == iDK) d = scale_of<KT>(kl + key * KS, b);
+        else if (ti == iDV) d = scale_of<VT>(vl + key * VS, b);
+        else if (ti == iMK) d = offset_of<KT>(kl + key * KS, b);
+        else d = offset_of<VT>(vl + key * VS, b);
+        dk_t[v] = d;
       }
       wave_sync();
     }
@@ -540,6 +635,13 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
           acc[1] = fmaf(dk.y, c[1], acc[1]);
           acc[2] = fmaf(dk.z, c[2], acc[2]);
           acc[3] = fmaf(dk.w, c[3], acc[3]);
+          if constexpr (KT == Q4_1) {
+            const float4 mk = *(const float4 *)(mk_t + b * 16 + 4 * g);
+            acc[0] = fmaf(mk.x, qblk[b], acc[0]);
+            acc[1] = fmaf(mk.y, qblk[b], acc[1]);
+            acc[2] = fmaf(mk.z, qblk[b], acc[2]);
+            acc[3] = fmaf(mk.w, qblk[b], acc[3]);
+          }
         }
       }
     }
@@ -568,6 +670,10 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       l_run *= corr;
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[i] *= corr;
+      if constexpr (VT == Q4_1) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b) cm[b] *= corr;
+      }
       m_run = m_new;
     }
     float psum = 0.0f;
@@ -612,10 +718,16 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         const half4 pf = __builtin_bit_cast(
             half4, u32x2{split_prod2(sc[0], dv.x, sc[1], dv.y, lo_mask),
                          split_prod2(sc[2], dv.z, sc[3], dv.w, lo_mask)});
+        if constexpr (VT == Q4_1) {
+          if (n < 8) {
+            const float4 mv = *(const float4 *)(mv_t + b * 16 + 4 * g);
+            cm[b] = fmaf(sc[0], mv.x, fmaf(sc[1], mv.y, fmaf(sc[2], mv.z, fmaf(sc[3], mv.w, cm[b]))));
+          }
+        }
         uint32_t u[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint8_t *vrow = vl + (4 * g + i) * VS + block_bytes(VT) * b + 2;
+          const uint8_t *vrow = vl + (4 * g + i) * VS + block_bytes(VT) * b + (VT == Q4_1 ? 4 : 2);
           u[i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
         }
         // [key0, key1] and [key2, key3] bytes of the lane's 2-dim (q8_0) or
@@ -632,7 +744,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
             a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) ^ 0x64806480u) + c);
             a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) ^ 0x64806480u) + c);
           } else {
-            const h2 c = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+            constexpr float kBias = VT == Q4_1 ? -1024.0f : -1032.0f;  // 1024 + (0 or 8)
+            const h2 c = {(_Float16)kBias, (_Float16)kBias};
             const int sh = 4 * e;
             a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ((w01_0 >> sh) & 0x000f000fu) | 0x64006400u) + c);
             a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ((w23_0 >> sh) & 0x000f000fu) | 0x64006400u) + c);
@@ -678,8 +791,19 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         *(floatx4 *)(dst + d0 + 4) = floatx4{o[2 * b][2], o[2 * b + 1][2], o[2 * b][3], o[2 * b + 1][3]};
       }
     } else {
+      if constexpr (VT == Q4_1) {
 #pragma unroll
-      for (int t = 0; t < 16; ++t) *(floatx4 *)(dst + v_dim<VT>(t, 4 * g)) = o[t];
+        for (int b = 0; b < 8; ++b) {
+          cm[b] += xor_f(cm[b], 16);
+          cm[b] += xor_f(cm[b], 32);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        floatx4 v = o[t];
+        if constexpr (VT == Q4_1) v += cm[t >> 1];
+        *(floatx4 *)(dst + v_dim<VT>(t, 4 * g)) = v;
+      }
     }
   }
   __syncthreads();
@@ -750,7 +874,9 @@ namespace {
 template <int KT, int VT>
 size_t decode_lds() {
   using TS = TileShape<KT, VT>;
-  const size_t tiles = (size_t)TS::WAVES * (TS::R * TS::TB + TS::DT) + kG * (kHD * 4 + 16);
+  // query rows (later the shared fragments and the q4_1 block sums)
+  const size_t qreg = (size_t)kG * (kHD * 4 + 16) + 256;
+  const size_t tiles = (size_t)TS::WAVES * (TS::R * TS::TB + TS::DT) + qreg;
   const size_t merge = (2 * TS::WAVES * kG + TS::WAVES * 16 * kRowPad + 2 * kG + TS::WAVES * kG + 4) * 4 +
                        (kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
   return tiles > merge ? tiles : merge;
@@ -764,14 +890,15 @@ hipError_t launch(const AttnArgs &a, int n_tok, hipStream_t st) {
   return hipGetLastError();
 }
 
-bool hot_type(int t) { return t == F16 || t == Q8_0 || t == Q4_0; }
+bool hot_k(int t) { return t == F16 || t == Q8_0 || t == Q4_0 || t == Q5_0 || t == Q4_1; }
+bool hot_v(int t) { return t == F16 || t == Q8_0 || t == Q4_0 || t == Q4_1; }
 
 }  // namespace
 
 bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim) {
   const char *e = std::getenv("RD4_DECODE_GENERIC");
   if (e && std::atoi(e) != 0) return false;
-  return hot_type(kt) && hot_type(vt) && head_dim == kHD && n_head_kv > 0 &&
+  return hot_k(kt) && hot_v(vt) && head_dim == kHD && n_head_kv > 0 &&
          n_head % n_head_kv == 0;
 }
 
@@ -797,6 +924,9 @@ hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hip
   RD4_D(F16, F16) RD4_D(F16, Q8_0) RD4_D(F16, Q4_0)
   RD4_D(Q8_0, F16) RD4_D(Q8_0, Q8_0) RD4_D(Q8_0, Q4_0)
   RD4_D(Q4_0, F16) RD4_D(Q4_0, Q8_0) RD4_D(Q4_0, Q4_0)
+  RD4_D(Q5_0, F16) RD4_D(Q5_0, Q8_0) RD4_D(Q5_0, Q4_0) RD4_D(Q5_0, Q4_1)
+  RD4_D(Q4_1, F16) RD4_D(Q4_1, Q8_0) RD4_D(Q4_1, Q4_0) RD4_D(Q4_1, Q4_1)
+  RD4_D(F16, Q4_1) RD4_D(Q8_0, Q4_1) RD4_D(Q4_0, Q4_1)
 #undef RD4_D
   if (err != hipSuccess || !a.ext_merge) return err;
   return merge_splits_launch(a, n_tok, st);

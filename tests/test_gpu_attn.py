@@ -166,32 +166,33 @@ def test_rope_kernel(rd4, orc, dev):
     assert np.linalg.norm(got[4] - want[4]) / np.linalg.norm(want[4]) < 2e-2
 
 
-@pytest.mark.parametrize("t", [1, 2, 3, 4])
-def test_decode_append_fused(rd4, orc, dev, t):
+@pytest.mark.parametrize("t,vt", [(1, 1), (2, 2), (3, 3), (4, 4), (4, 5), (5, 5), (5, 2)])
+def test_decode_append_fused(rd4, orc, dev, t, vt):
     """rd4_attn_decode_append == kv_store of the new row + gated decode."""
     import torch
     nh, nkv, hd, n = 24, 4, 256, 777
-    rb = orc.row_bytes(t, hd)
+    rb, vrb = orc.row_bytes(t, hd), orc.row_bytes(vt, hd)
     k = make_cache(orc, t, n, nkv, hd, 100)
-    v = make_cache(orc, t, n, nkv, hd, 101)
+    v = make_cache(orc, vt, n, nkv, hd, 101)
     kn, vn = orc.randn(nkv * hd, 102), orc.randn(nkv * hd, 103)
     k_ref, v_ref = k.copy(), v.copy()
     k_ref[(n - 1) * nkv * rb:] = orc.store_rows(t, kn)
-    v_ref[(n - 1) * nkv * rb:] = orc.store_rows(t, vn)
+    v_ref[(n - 1) * nkv * vrb:] = orc.store_rows(vt, vn)
     k[(n - 1) * nkv * rb:] = 0x5A  # stale row content must be replaced
-    v[(n - 1) * nkv * rb:] = 0xA5
+    v[(n - 1) * nkv * vrb:] = 0xA5
     q, g = orc.randn(nh * hd, 104), orc.randn(nh * hd, 105)
-    gs, want = orc.sigmoid_gate(g, orc.attn_decode(q, k_ref, v_ref, n - 1, nh, nkv, hd, 1 / 16, t, t).ravel())
+    gs, want = orc.sigmoid_gate(g, orc.attn_decode(q, k_ref, v_ref, n - 1, nh, nkv, hd, 1 / 16, t, vt).ravel())
     kd, vd, gd = to_dev(k, torch, dev), to_dev(v, torch, dev), to_dev(g, torch, dev)
     out = torch.empty(nh * hd, device=dev)
     rd4.attn_decode_append(to_dev(q, torch, dev), to_dev(kn, torch, dev), to_dev(vn, torch, dev), kd, vd,
-                           out, n - 1, nh, nkv, hd, 1 / 16, t, t, gate=gd)
+                           out, n - 1, nh, nkv, hd, 1 / 16, t, vt, gate=gd)
     torch.cuda.synchronize()
     assert np.array_equal(kd.cpu().numpy(), k_ref) and np.array_equal(vd.cpu().numpy(), v_ref)
-    check_close(out.cpu().numpy(), want, "append %d" % t)
+    check_close(out.cpu().numpy(), want, "append %d/%d" % (t, vt))
 
 
-@pytest.mark.parametrize("kt,vt", [(1, 1), (2, 2), (3, 3), (2, 3), (1, 2)])
+@pytest.mark.parametrize("kt,vt", [(1, 1), (2, 2), (3, 3), (2, 3), (1, 2), (4, 5), (5, 5), (4, 2),
+                                   (5, 3), (1, 5), (2, 5), (4, 1)])
 def test_mfma_path_matches_generic_path(rd4, orc, dev, kt, vt, monkeypatch):
     """The MFMA decode kernel and the all-types kernel agree (both vs the oracle)."""
     import torch
@@ -207,15 +208,17 @@ def test_mfma_path_matches_generic_path(rd4, orc, dev, kt, vt, monkeypatch):
     check_close(got_gen, want, "generic")
 
 
-@pytest.mark.parametrize("cfg", ["f16_32k_gate", "q8_0_32k_append", "q4_0_131k"])
+@pytest.mark.parametrize("cfg", ["f16_32k_gate", "q8_0_32k_append", "q4_0_131k", "q5_0_q4_1_131k"])
 def test_baseline_decode_configs_full_size(rd4, orc, dev, cfg):
-    """BASELINE configs[1..3] at their real shapes vs the f64 oracle."""
+    """BASELINE configs[1..3] at their real shapes vs the f64 oracle, and the
+    reference's 131K default pair (K q5_0, V q4_1) at the same shape."""
     import torch
     nh, nkv, hd = 24, 4, 256
-    kt = {"f16_32k_gate": 1, "q8_0_32k_append": 2, "q4_0_131k": 3}[cfg]
-    n = 131001 if kt == 3 else 32768
+    kt, vt = {"f16_32k_gate": (1, 1), "q8_0_32k_append": (2, 2), "q4_0_131k": (3, 3),
+              "q5_0_q4_1_131k": (4, 5)}[cfg]
+    n = 131001 if kt >= 3 else 32768
     k = make_cache(orc, kt, n, nkv, hd, 120, outlier=(kt == 2))
-    v = make_cache(orc, kt, n, nkv, hd, 121, outlier=(kt == 2))
+    v = make_cache(orc, vt, n, nkv, hd, 121, outlier=(kt == 2))
     q, g = orc.randn(nh * hd, 122), orc.randn(nh * hd, 123)
     kd, vd = to_dev(k, torch, dev), to_dev(v, torch, dev)
     out = torch.empty(nh * hd, device=dev)
@@ -228,7 +231,7 @@ def test_baseline_decode_configs_full_size(rd4, orc, dev, cfg):
         rd4.attn_decode_append(to_dev(q, torch, dev), to_dev(kn, torch, dev), to_dev(vn, torch, dev), kd,
                                vd, out, n - 1, nh, nkv, hd, 1 / 16, kt, kt, gate=gd)
     else:
-        rd4.attn_decode(to_dev(q, torch, dev), kd, vd, out, n - 1, nh, nkv, hd, 1 / 16, kt, kt, gate=gd)
+        rd4.attn_decode(to_dev(q, torch, dev), kd, vd, out, n - 1, nh, nkv, hd, 1 / 16, kt, vt, gate=gd)
     torch.cuda.synchronize()
-    _, want = orc.sigmoid_gate(g, orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, kt, kt, threads=8).ravel())
+    _, want = orc.sigmoid_gate(g, orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, kt, vt, threads=8).ravel())
     check_close(out.cpu().numpy(), want, cfg)
