@@ -1,5 +1,5 @@
-// Split-KV GQA decode on f16 MFMA (gfx950). K in f16, q8_0, q4_0, q5_0 or
-// q4_1; V in f16, q8_0, q4_0 or q4_1.
+// Split-KV GQA decode on f16 MFMA (gfx950), K and V each in f16, q8_0, q4_0,
+// q5_0 or q4_1 (f32 caches take the all-types kernel).
 //
 // Reference semantics: attn_split_kernel + attn_merge_kernel and the batched
 // forms (include/rdna4/attn.cuh:445-590, 686-845) with the output gate of
@@ -274,7 +274,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // operand lane with MFMA row r reads whole aligned words of its 4 keys:
 //   f16:  16-byte chunk r + 16h (dims 8(r + 16h) .. +7), one MFMA per dim, t = 8h + e;
 //   q8_0: the 2 bytes at dims 32b + 2r, +1 of block b, t = 2b + e;
-//   q4_0, q4_1: byte r of block b (element r low nibble, r + 16 high), t = 2b + e;
+//   q4_0, q4_1, q5_0: byte r of block b (element r low nibble, r + 16 high;
+//   q5_0 adds high bits r and r + 16), t = 2b + e;
 // so every MFMA's rows lie in one quantization block and share one P' operand.
 template <int VT>
 __host__ __device__ constexpr int v_dim(int t, int r) {
@@ -727,8 +728,15 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         uint32_t u[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint8_t *vrow = vl + (4 * g + i) * VS + block_bytes(VT) * b + (VT == Q4_1 ? 4 : 2);
+          const uint8_t *blk = vl + (4 * g + i) * VS + block_bytes(VT) * b;
+          const uint8_t *vrow = blk + (VT == Q4_1 ? 4 : VT == Q5_0 ? 6 : 2);
           u[i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
+          if constexpr (VT == Q5_0) {
+            // element n: low nibble + high bit n; element n + 16: high nibble +
+            // high bit n + 16; as two 5-bit values in bytes 0 and 1
+            const uint32_t hlo = (lds_u16(blk + 2) >> n) & 1u, hhi = (lds_u16(blk + 4) >> n) & 1u;
+            u[i] = (u[i] & 0x0fu) | (hlo << 4) | ((u[i] & 0xf0u) << 4) | (hhi << 12);
+          }
         }
         // [key0, key1] and [key2, key3] bytes of the lane's 2-dim (q8_0) or
         // 2-nibble (q4_0) word, one MFMA per dim
@@ -738,7 +746,12 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           uint32_t a01, a23;
-          if constexpr (VT == Q8_0) {
+          if constexpr (VT == Q5_0) {
+            const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
+            const h2 c = {(_Float16)-1040.0f, (_Float16)-1040.0f};  // 1024 + 16
+            a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) | 0x64006400u) + c);
+            a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) | 0x64006400u) + c);
+          } else if constexpr (VT == Q8_0) {
             const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
             const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
             a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) ^ 0x64806480u) + c);
@@ -891,7 +904,7 @@ hipError_t launch(const AttnArgs &a, int n_tok, hipStream_t st) {
 }
 
 bool hot_k(int t) { return t == F16 || t == Q8_0 || t == Q4_0 || t == Q5_0 || t == Q4_1; }
-bool hot_v(int t) { return t == F16 || t == Q8_0 || t == Q4_0 || t == Q4_1; }
+bool hot_v(int t) { return t == F16 || t == Q8_0 || t == Q4_0 || t == Q5_0 || t == Q4_1; }
 
 }  // namespace
 
@@ -927,6 +940,7 @@ hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hip
   RD4_D(Q5_0, F16) RD4_D(Q5_0, Q8_0) RD4_D(Q5_0, Q4_0) RD4_D(Q5_0, Q4_1)
   RD4_D(Q4_1, F16) RD4_D(Q4_1, Q8_0) RD4_D(Q4_1, Q4_0) RD4_D(Q4_1, Q4_1)
   RD4_D(F16, Q4_1) RD4_D(Q8_0, Q4_1) RD4_D(Q4_0, Q4_1)
+  RD4_D(F16, Q5_0) RD4_D(Q8_0, Q5_0) RD4_D(Q4_0, Q5_0) RD4_D(Q5_0, Q5_0) RD4_D(Q4_1, Q5_0)
 #undef RD4_D
   if (err != hipSuccess || !a.ext_merge) return err;
   return merge_splits_launch(a, n_tok, st);

@@ -192,7 +192,7 @@ def test_decode_append_fused(rd4, orc, dev, t, vt):
 
 
 @pytest.mark.parametrize("kt,vt", [(1, 1), (2, 2), (3, 3), (2, 3), (1, 2), (4, 5), (5, 5), (4, 2),
-                                   (5, 3), (1, 5), (2, 5), (4, 1)])
+                                   (5, 3), (1, 5), (2, 5), (4, 1), (4, 4), (5, 4), (1, 4)])
 def test_mfma_path_matches_generic_path(rd4, orc, dev, kt, vt, monkeypatch):
     """The MFMA decode kernel and the all-types kernel agree (both vs the oracle)."""
     import torch
