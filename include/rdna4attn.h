@@ -143,6 +143,18 @@ int rd4_attn_decode_append(const float *q, const float *k_new, const float *v_ne
                            void *v, float *out, float *gate, int t, int n_head, int n_head_kv,
                            int head_dim, float scale, int kt, int vt, int n_splits, void *stream);
 
+/* Native multi-token decode (the MTP verify step: N = D+1 drafted tokens,
+ * graph.cuh:1494-1527 through attn_split_batch_launch; mtp.cuh:585-596 for the
+ * draft token itself): tokens i = 0..n_tok-1 sit at consecutive positions
+ * t0 + i and token i attends keys 0..t0+i (the rows were appended before the
+ * call). q/out/gate are [n_tok][n_head][head_dim]; gate may be NULL, else
+ * fused as in rd4_attn_decode. n_splits = 0 picks the split count for the GPU
+ * from the token count; n_splits >= 1 forces it. Each token's result is
+ * bit-identical to rd4_attn_decode of that token with the same forced split count. */
+int rd4_attn_decode_tokens(const float *q, const void *k, const void *v, float *out, float *gate,
+                           int t0, int n_tok, int n_head, int n_head_kv, int head_dim, float scale,
+                           int kt, int vt, int n_splits, void *stream);
+
 /* ---- batched attention (attn.cuh:373-424, 958-1049) ---------------------- */
 
 /* attn_batch_launch (attn.cuh:373): token i of n_tok attends keys 0..pos[i]

@@ -46,6 +46,7 @@ SIGNATURES = {
     "rd4_prefill": ([_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I),
     "rd4_sigmoid_gate_launch": ([_P, _P, _I64, _P], _I),
     "rd4_rope_launch": ([_P, _I, _I, _I, _I, _F, _P, _P], _I),
+    "rd4_attn_decode_tokens": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
     "rd4_rms_norm_launch": ([_P, _P, _P, _I64, _I64, _F, _P], _I),
     "rd4_qk_norm_rope_append": ([_P, _P, _P, _P, _P, _F, _I, _F, _P, _I, _I, _I, _I, _P, _P, _P,
                                  _P, _P, _I, _I, _P], _I),
@@ -159,6 +160,14 @@ def attn_decode_append(q, k_new, v_new, k, v, out, t, n_head, n_head_kv, head_di
     _check(lib().rd4_attn_decode_append(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k), _ptr(v), _ptr(out),
                                         _ptr(gate), t, n_head, n_head_kv, head_dim, scale, kt, vt,
                                         n_splits, _stream()), "attn_decode_append")
+
+
+def attn_decode_tokens(q, k, v, out, t0, n_tok, n_head, n_head_kv, head_dim, scale, kt, vt,
+                       gate=None, n_splits=0):
+    """Multi-token decode: token i at position t0 + i attends keys 0..t0+i."""
+    _check(lib().rd4_attn_decode_tokens(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(gate), t0, n_tok,
+                                        n_head, n_head_kv, head_dim, scale, kt, vt, n_splits,
+                                        _stream()), "attn_decode_tokens")
 
 
 def attn_launch(q, k, v, out, t, n_head, n_head_kv, head_dim, scale, kt, vt):

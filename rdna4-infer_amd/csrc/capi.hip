@@ -122,8 +122,10 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   const bool mfma = aligned16 && decode_mfma_supported(kt, vt, n_head, n_head_kv, head_dim);
   if (splits <= 0) {  // automatic, at least -splits
     const int min_s = -splits;
-    splits = mfma ? auto_splits(t + 1, n_head_kv * n_chunks, 256, 64)
-                  : auto_splits(t + 1, n_head_kv * n_chunks, 1024, 64);
+    // CTAs per split: every token's (kv head, head chunk) pairs; the keys of
+    // the first token bound the split count
+    const int per_split = n_head_kv * n_chunks * n_tok;
+    splits = mfma ? auto_splits(t + 1, per_split, 256, 64) : auto_splits(t + 1, per_split, 1024, 64);
     if (splits < min_s) splits = min_s;
   }
   if (splits < 1) splits = 1;
@@ -297,6 +299,15 @@ int rd4_attn_decode_append(const float *q, const float *k_new, const float *v_ne
     return fail(RD4_EINVAL, "cache pointers misaligned%s");
   return run_attn(q, k, v, out, gate, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt, vt,
                   n_splits, (hipStream_t)stream, k_new, v_new);
+}
+
+int rd4_attn_decode_tokens(const float *q, const void *k, const void *v, float *out, float *gate,
+                           int t0, int n_tok, int n_head, int n_head_kv, int head_dim, float scale,
+                           int kt, int vt, int n_splits, void *stream) {
+  if (n_splits < 0 || n_tok < 1 || t0 < 0)
+    return fail(RD4_EINVAL, "need n_tok >= 1, t0 >= 0 and n_splits >= 0%s");
+  return run_attn(q, k, v, out, gate, nullptr, t0, n_tok, n_head, n_head_kv, head_dim, scale, kt,
+                  vt, n_splits, (hipStream_t)stream);
 }
 
 int rd4_attn_launch(const float *q, const void *k, const void *v, float *out, int t, int n_head,
