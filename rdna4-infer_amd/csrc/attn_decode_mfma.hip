@@ -354,7 +354,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const int kvh = blockIdx.y / a.n_chunks;
   const int hc = blockIdx.y - kvh * a.n_chunks;
   const int tok = blockIdx.z;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // the wave index is uniform across the wave: readfirstlane lets the compiler
+  // keep tile bases and LDS destinations in scalar registers
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
 #if RD4_DEC_TRACE
   // timestamps of CTA (0,0): slot [w][point] in a.out as u64 (diagnostic builds only)
