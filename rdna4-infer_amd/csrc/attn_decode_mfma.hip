@@ -331,6 +331,17 @@ __device__ __forceinline__ uint32_t split_prod2(float p0, float d0, float p1, fl
           : "v"(p0), "v"(d0), "v"(m), "v"(p1), "v"(d1));
   return r;
 }
+#ifndef RD4_DEC_PV_HILO
+#define RD4_DEC_PV_HILO 0
+#endif
+// f16 of four products in the rows n < 8 (lo_mask = 0 there) and zero in the
+// rows n >= 8, as the B operand of one PV MFMA.
+__device__ __forceinline__ half4 hi_only4(float x0, float x1, float x2, float x3, uint32_t lo_mask) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 a = {(_Float16)x0, (_Float16)x1}, b = {(_Float16)x2, (_Float16)x3};
+  return __builtin_bit_cast(half4, u32x2{__builtin_bit_cast(uint32_t, a) & ~lo_mask,
+                                         __builtin_bit_cast(uint32_t, b) & ~lo_mask});
+}
 // Online-softmax reference max: moved only when a row's new scores exceed it
 // by more than kRescaleLog2 (probabilities stay <= 2^8 against a stale max),
 // so the O rescale and the cross-lane max are rare instead of per tile.
@@ -439,17 +450,17 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   };
   // Full tiles use offsets computed once: instructions whose 64 chunks are all
   // K (or all V) address from a wave-uniform base.
-  int goff[NI];
+  uint32_t goff[NI];  // unsigned: scalar base + 32-bit vector offset addressing
 #pragma unroll
   for (int r = 0; r < NI; ++r) {
     const int c = lane + 64 * r;
     if (c < KCH) {
       const int row = c / KC, slot = c - row * KC;
-      goff[r] = row * (int)kstride + 16 * swz<KT>(row, slot);
+      goff[r] = (uint32_t)(row * (int)kstride + 16 * swz<KT>(row, slot));
     } else {
       const int cv = c < KCH + VCH ? c - KCH : 0;
       const int row = cv / VC, slot = cv - row * VC;
-      goff[r] = row * (int)vstride + 16 * swz<VT>(row, slot);
+      goff[r] = (uint32_t)(row * (int)vstride + 16 * swz<VT>(row, slot));
     }
   }
   auto issue = [&](int i) {  // i-th tile of this wave
@@ -693,9 +704,13 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       o[0][0] += sc[0] + sc[3];
       (void)vl;
     } else if constexpr (VT == F16) {
+#if RD4_DEC_PV_HILO
       const half4 pf = __builtin_bit_cast(
           half4, u32x2{split_prod2(sc[0], 1.0f, sc[1], 1.0f, lo_mask),
                        split_prod2(sc[2], 1.0f, sc[3], 1.0f, lo_mask)});
+#else
+      const half4 pf = hi_only4(sc[0], sc[1], sc[2], sc[3], lo_mask);
+#endif
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         // 16-byte chunk n + 16h (dims 8(n + 16h) .. +7) of the lane's 4 keys
@@ -718,9 +733,14 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
         const float4 dv = *(const float4 *)(dv_t + b * 16 + 4 * g);
+#if RD4_DEC_PV_HILO
         const half4 pf = __builtin_bit_cast(
             half4, u32x2{split_prod2(sc[0], dv.x, sc[1], dv.y, lo_mask),
                          split_prod2(sc[2], dv.z, sc[3], dv.w, lo_mask)});
+#else
+        // P' = f16(p * d) in the hi rows, zero in the lo rows
+        const half4 pf = hi_only4(sc[0] * dv.x, sc[1] * dv.y, sc[2] * dv.z, sc[3] * dv.w, lo_mask);
+#endif
         if constexpr (VT == Q4_1) {
           if (n < 8) {
             const float4 mv = *(const float4 *)(mv_t + b * 16 + 4 * g);
