@@ -13,7 +13,7 @@
 // rows (one MFMA slab), two waves per SIMD so one wave's softmax overlaps
 // another's MFMAs. The CTA walks 64-key blocks:
 //   * K block (64 x 256 f16) arrives by global->LDS DMA, row-major with the
-//     16-byte chunks of row r XOR-swizzled by swz(r) (conflict-free reads);
+//     16-byte chunks of row r XOR-swizzled by r & 15 (conflict-free reads);
 //   * V block arrives the same way, same swizzle; the PV operand (16 dims x
 //     8 keys per lane group) is read straight out of it with the gfx950
 //     transposing LDS load (ds_read_b64_tr_b16), so no transpose pass;
@@ -57,13 +57,6 @@ constexpr int kLdsBytes = 4 * kKBytes;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ _Float16 h16(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
-
-// LDS slot of 16-byte chunk c of key row j is c ^ swz(j). Rows are 512 B, so
-// every row starts on bank 0; swz moves key bits 0-2 to chunk bits 1-3 and key
-// bit 3 to chunk bit 0. Both read patterns then hit distinct banks: the K
-// operand (16 lanes = 16 consecutive keys, one chunk each) and the transposing
-// V read (32 lanes = 8 consecutive keys x 2 chunks x two 8-byte halves).
-__device__ __forceinline__ int swz(int j) { return ((j & 7) << 1) | ((j >> 3) & 1); }
 
 }  // namespace
 
@@ -178,14 +171,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   }
 
   // ---- block loads. K: 2048 chunks of 16 B per block = 8 DMA instructions per
-  // lane; chunk c -> key c/32, LDS slot c%32 holds global column slot^swz(key).
+  // lane; chunk c -> key c/32, LDS slot c%32 holds global column slot^(key&15).
   // Per-lane offsets are block-invariant and computed once.
   int k_goff[kNDMA];  // byte offset of this lane's chunk r from the block's first key
 #pragma unroll
   for (int r = 0; r < kNDMA; ++r) {
     const int c = (w * kNDMA + r) * 64 + lane;
     const int key = c >> 5, slot = c & 31;
-    k_goff[r] = key * (int)kvstride + 16 * (slot ^ swz(key));
+    k_goff[r] = key * (int)kvstride + 16 * (slot ^ (key & 15));
   }
   auto issue_k = [&](int blk, int stage) {
     uint8_t *kd = smem + stage * kKBytes;
@@ -203,7 +196,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
         const int key = c >> 5, slot = c & 31;
         const int jk = min(j0 + key, kend);
         __builtin_amdgcn_global_load_lds(
-            (const void *)(kbase + (int64_t)jk * kvstride + 16 * (slot ^ swz(key))),
+            (const void *)(kbase + (int64_t)jk * kvstride + 16 * (slot ^ (key & 15))),
             (lds_void *)(kd + (w * kNDMA + r) * 1024), 16, 0, 0);
       }
     }
@@ -225,7 +218,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
         const int key = c >> 5, slot = c & 31;
         const int jk = min(j0 + key, kend);
         __builtin_amdgcn_global_load_lds(
-            (const void *)(vbase + (int64_t)jk * kvstride + 16 * (slot ^ swz(key))),
+            (const void *)(vbase + (int64_t)jk * kvstride + 16 * (slot ^ (key & 15))),
             (lds_void *)(vd + (w * kNDMA + r) * 1024), 16, 0, 0);
       }
     }
@@ -236,12 +229,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   // of 16 apart from the lane group's 4g), so the per-lane part is fixed.
   const int tr_kx = 4 * g + (n >> 2);                       // key & 15 of this source lane
   const int tr_off = tr_kx * (kHD * 2) + 8 * (n & 1);        // row and 8-byte half
-  const int tr_m = 16 * ((n >> 1 & 1) ^ swz(tr_kx));        // swizzle term of the chunk
+  const int tr_m = 16 * ((n >> 1 & 1) ^ tr_kx);             // swizzle term of the chunk
   // LDS read offsets of the MFMA operands (block-invariant).
   // K: key 16kt + n, dims 32b + 8g: slot (4b + g) ^ n = 4(b ^ (n>>2)) + (g ^ (n&3)).
   int k_loff[8];
 #pragma unroll
-  for (int b = 0; b < 8; ++b) k_loff[b] = n * (kHD * 2) + 16 * ((4 * b + g) ^ swz(n));
+  for (int b = 0; b < 8; ++b) k_loff[b] = n * (kHD * 2) + 64 * (b ^ (n >> 2)) + 16 * (g ^ (n & 3));
 
   if (n_blocks > 0) {
     issue_k(0, 0);
