@@ -130,6 +130,28 @@ def decode_workload(torch, rd4, kt, ctx, outlier, gated=True, vt=None):
     return step, step, step_bytes, attn_bytes, cpu, info
 
 
+def tokens_workload(torch, rd4, kt=2, ctx=32768, n_tok=4):
+    """MTP verify step: n_tok consecutive tokens ending at key ctx-1 attend (gated)
+    in one rd4_attn_decode_tokens launch; bytes = the K/V rows the tokens span
+    (read once would be ideal; each token reads them today)."""
+    krb = rd4.kv_row_bytes(kt, HD)
+    kc = make_cache(torch, rd4, kt, ctx, SEED, True)
+    vc = make_cache(torch, rd4, kt, ctx, SEED + 1, True)
+    g = torch.Generator(device="cuda").manual_seed(SEED + 4)
+    q = torch.randn(n_tok * NH * HD, generator=g, device="cuda")
+    gate = torch.randn(n_tok * NH * HD, generator=g, device="cuda")
+    out = torch.empty_like(q)
+
+    def step():
+        rd4.attn_decode_tokens(q, kc, vc, out, ctx - n_tok, n_tok, NH, NKV, HD, 1.0 / 16, kt, kt,
+                               gate=gate)
+
+    kv_bytes = ctx * NKV * 2 * krb + n_tok * NH * HD * 4 * 4
+    info = {"workload": "decode_tokens", "kv_type": rd4.TYPE_NAMES[kt], "ctx": ctx, "n_tok": n_tok,
+            "n_head": NH, "n_head_kv": NKV, "head_dim": HD, "gate": True, "seed": SEED}
+    return step, step, kv_bytes, kv_bytes, None, info
+
+
 def prefill_workload(torch, rd4, n_prefix=4096, n_q=4096):
     """4096 f16 queries at positions 4096..8191 over an f16 cache of
     8192 rows (prefix + the chunk), causal, gated; the chunk's K/V rows are also
@@ -203,7 +225,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode_q8_0",
                     choices=["decode_q8_0", "decode_f16", "decode_q4_0", "decode_q5_0_q4_1",
-                             "prefill", "copy"])
+                             "decode_tokens", "prefill", "copy"])
     ap.add_argument("--extra", action="store_true", help="also measure the other configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
@@ -236,6 +258,8 @@ def main():
             return decode_workload(torch, rd4, 3, 131001, False)
         if name == "decode_q5_0_q4_1":  # the reference's 131K default pair
             return decode_workload(torch, rd4, 4, 131001, False, vt=5)
+        if name == "decode_tokens":  # MTP verify: 4 tokens at 32K, q8_0
+            return tokens_workload(torch, rd4)
         return prefill_workload(torch, rd4)
 
     step, dom, step_units, dom_units, cpu, info = build(args.workload)
@@ -266,14 +290,14 @@ def main():
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
            "data": "synthetic (seeded N(0,1), random K/V/Q/gate)", "config": info,
            "roofline": roof}
-    if not args.no_cpu:
+    if not args.no_cpu and cpu is not None:
         v, sample = cpu()
         res["cpu_baseline"] = {"value": round(v, 4), "unit": unit, "cores": 1, "kind": "port",
                                "sample": sample + " (oracle/oracle.c, f64 accumulate)",
                                "host_nproc": os.cpu_count()}
     if args.extra:
         res["extra"] = {}
-        for name in ("decode_f16", "decode_q4_0", "decode_q5_0_q4_1", "prefill"):
+        for name in ("decode_f16", "decode_q4_0", "decode_q5_0_q4_1", "decode_tokens", "prefill"):
             if name == args.workload:
                 continue
             st, dm, su, du, _, inf = build(name)

@@ -149,8 +149,11 @@ int rd4_attn_decode_append(const float *q, const float *k_new, const float *v_ne
  * t0 + i and token i attends keys 0..t0+i (the rows were appended before the
  * call). q/out/gate are [n_tok][n_head][head_dim]; gate may be NULL, else
  * fused as in rd4_attn_decode. n_splits = 0 picks the split count for the GPU
- * from the token count; n_splits >= 1 forces it. Each token's result is
- * bit-identical to rd4_attn_decode of that token with the same forced split count. */
+ * from the token count; n_splits >= 1 forces it. On the MFMA path (hd 256,
+ * GQA group <= 8) one CTA carries two consecutive tokens, so every K/V tile is
+ * read and converted once per pair; those queries enter the products as f16
+ * (results within the attention tolerance, not bit-identical to per-token
+ * decode; rd4_attn_split_batch_launch keeps that identity). */
 int rd4_attn_decode_tokens(const float *q, const void *k, const void *v, float *out, float *gate,
                            int t0, int n_tok, int n_head, int n_head_kv, int head_dim, float scale,
                            int kt, int vt, int n_splits, void *stream);

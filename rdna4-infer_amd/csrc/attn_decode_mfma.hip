@@ -352,7 +352,7 @@ constexpr float kRescaleLog2 = RD4_DEC_THRESH;
 
 }  // namespace
 
-template <int KT, int VT>
+template <int KT, int VT, bool PAIR>
 __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfma_kernel(AttnArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   using TS = TileShape<KT, VT>;
@@ -364,7 +364,11 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const int s = blockIdx.x;
   const int kvh = blockIdx.y / a.n_chunks;
   const int hc = blockIdx.y - kvh * a.n_chunks;
-  const int tok = blockIdx.z;
+  // Pair mode: this CTA carries tokens tok and tok + 1 (ntc of them exist);
+  // MFMA row n is head n & 7 of token tok + (n >> 3), queries in f16.
+  constexpr bool pair = PAIR;
+  const int tok = pair ? 2 * (int)blockIdx.z : (int)blockIdx.z;
+  const int ntc = pair ? min(2, a.n_tok - tok) : 1;
   // the wave index is uniform across the wave: readfirstlane lets the compiler
   // keep tile bases and LDS destinations in scalar registers
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -386,7 +390,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const int grp = a.n_head / a.n_head_kv;
   const int h0 = kvh * grp + hc * kG;
   const int G = min(kG, grp - hc * kG);
-  const int t = a.pos ? a.pos[tok] : a.t + tok;
+  const int t = a.pos ? a.pos[tok] : a.t + tok + ntc - 1;  // last key of the CTA's last token
   const int n_keys = t + 1;
 
   int chunk = (max(n_keys, 0) + a.n_splits - 1) / a.n_splits;
@@ -505,20 +509,20 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       }
     }
   };
-  issue_q();
+  if (!pair) issue_q();
   if (!owns_new) {
 #pragma unroll
     for (int i = 0; i < R - 1; ++i)
       if (i < my_tiles) issue(i);  // first tiles in flight right behind the query rows
   }
   // this wave's query chunk has landed once at most the tile loads issued after it remain
-  {
+  if (!pair) {
     const int after = owns_new ? 0 : min(R - 1, my_tiles);
     if (after >= 2) wait_vm<2 * NI>();
     else if (after == 1) wait_vm<NI>();
     else wait_vm<0>();
+    __syncthreads();
   }
-  __syncthreads();
   RD4_TP();
   if (owns_new) {
 #pragma unroll
@@ -533,7 +537,28 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const uint32_t lo_mask = n >= 8 ? 0xffffffffu : 0u;
   half8 qf[8];
   float qblk[8];
-  {
+  if (pair) {
+    // f16 query rows straight from global memory, both tokens' heads
+    const int hh = n & 7, tr = n >> 3;
+    const bool on = hh < G && tr < ntc;
+    const float *qrow = a.q + ((int64_t)(tok + (on ? tr : 0)) * a.n_head + h0 + (on ? hh : 0)) * kHD;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      float qs = 0.0f;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float2 f = on ? *(const float2 *)(qrow + k_dim<KT>(b, g, 2 * jj)) : make_float2(0.f, 0.f);
+        qf[b][2 * jj] = (_Float16)f.x;
+        qf[b][2 * jj + 1] = (_Float16)f.y;
+        if constexpr (KT == Q4_1) qs += f.x + f.y;
+      }
+      if constexpr (KT == Q4_1) {
+        qs += xor_f(qs, 16);
+        qs += xor_f(qs, 32);
+        qblk[b] = qs;
+      }
+    }
+  } else {
     const int hh = n & 7;
     const bool on = hh < G;
     const uint8_t *qrow = q_lds + (on ? hh : 0) * qsb;
@@ -585,6 +610,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   // edge gather of the unaligned quantized-K blocks: lane group 3 (q8_0) or
   // the odd lane groups (q4_0) take the block's first and last byte pairs
   const uint32_t sel_edge = (KT == Q8_0 ? g == 3 : (g & 1) == 1) ? 0x05040302u : 0x07060504u;
+  // pair mode: the last key of this lane's row; the P operand fills all 16 rows
+  const int row_last = pair ? a.t + tok + (n >> 3) : t;
+  const uint32_t pmask = pair ? 0u : lo_mask;
 
   floatx4 o[16];
 #pragma unroll
@@ -665,11 +693,13 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     // all four adds, so the exchange stays a plain lane shuffle.)
     float sc[4];
     bool over = false;
+    // last key this lane's row may see, relative to the tile: pair mode masks the
+    // second token's last key in the first token's rows
+    const int lim = pair ? min(nk - 1, row_last - (j_begin + (w + i * kWaves) * kTile)) : nk - 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float other = xor_f(acc[i], 8);
-      float v = (acc[i] + other) * sl2;
-      if (4 * g + i >= nk) v = -INFINITY;
+      float v = pair ? acc[i] * sl2 : (acc[i] + xor_f(acc[i], 8)) * sl2;
+      if (4 * g + i > lim) v = -INFINITY;
       sc[i] = v;
       over |= v > m_run + kRescaleLog2;
     }
@@ -680,7 +710,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       tmax = fmaxf(tmax, xor_f(tmax, 16));
       tmax = fmaxf(tmax, xor_f(tmax, 32));
       const float m_new = fmaxf(m_run, tmax);
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      // a row whose max did not move (also -inf, a row with no key yet) keeps its state
+      const float corr = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= corr;
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[i] *= corr;
@@ -691,9 +722,12 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       m_run = m_new;
     }
     float psum = 0.0f;
+    // a row that has seen no key yet (pair mode, a split holding only the
+    // second token's last key) keeps m_run = -inf; its masked scores give 0
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);
+      sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_use);
       psum += sc[i];
     }
     l_run += psum;
@@ -709,7 +743,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
           half4, u32x2{split_prod2(sc[0], 1.0f, sc[1], 1.0f, lo_mask),
                        split_prod2(sc[2], 1.0f, sc[3], 1.0f, lo_mask)});
 #else
-      const half4 pf = hi_only4(sc[0], sc[1], sc[2], sc[3], lo_mask);
+      const half4 pf = hi_only4(sc[0], sc[1], sc[2], sc[3], pmask);
 #endif
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -739,10 +773,10 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
                          split_prod2(sc[2], dv.z, sc[3], dv.w, lo_mask)});
 #else
         // P' = f16(p * d) in the hi rows, zero in the lo rows
-        const half4 pf = hi_only4(sc[0] * dv.x, sc[1] * dv.y, sc[2] * dv.z, sc[3] * dv.w, lo_mask);
+        const half4 pf = hi_only4(sc[0] * dv.x, sc[1] * dv.y, sc[2] * dv.z, sc[3] * dv.w, pmask);
 #endif
         if constexpr (VT == Q4_1) {
-          if (n < 8) {
+          if (pair || n < 8) {
             const float4 mv = *(const float4 *)(mv_t + b * 16 + 4 * g);
             cm[b] = fmaf(sc[0], mv.x, fmaf(sc[1], mv.y, fmaf(sc[2], mv.z, fmaf(sc[3], mv.w, cm[b]))));
           }
@@ -798,13 +832,16 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   l_run += xor_f(l_run, 16);
   l_run += xor_f(l_run, 32);
 
-  // ---- merge the waves through LDS (reuses the tile buffers)
+  // ---- merge the waves through LDS (reuses the tile buffers). Row slots are
+  // the 16 MFMA rows: single-token mode uses rows 0-7 (heads) and adds the lo
+  // rows 8-15 into them; pair mode keeps all 16 (two tokens' heads).
   __syncthreads();
-  float *wm = (float *)smem;                 // [kWaves][kG] m, then [kWaves][kG] l
-  float *wo = wm + 2 * kWaves * kG;          // [kWaves][16 rows][kRowPad]
-  if (lane < kG) {
-    wm[w * kG + lane] = m_run;
-    wm[kWaves * kG + w * kG + lane] = l_run;
+  constexpr int kR = 16;
+  float *wm = (float *)smem;                 // [kWaves][kR] m, then [kWaves][kR] l
+  float *wo = wm + 2 * kWaves * kR;          // [kWaves][16 rows][kRowPad]
+  if (lane < kR) {
+    wm[w * kR + lane] = m_run;
+    wm[kWaves * kR + w * kR + lane] = l_run;
   }
   {
     // o[t][i] holds dim v_dim<VT>(t, 4g + i); written back as 4-dim runs
@@ -843,43 +880,50 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   }
   __syncthreads();
   RD4_TP();
-  float *ms = wo + kWaves * 16 * kRowPad;  // [kG] m (ln units), [kG] L, [kWaves][kG] weights
-  if (tid < kWaves * kG) {
-    // thread (wave ww, head hh); the max and the weighted sum run over ww
-    // (lane bits 3..) with lane exchanges, no serial loop
-    const int hh = tid % kG, ww = tid / kG;
-    const float mw = wm[ww * kG + hh];
-    float mm = mw;
+  float *ms = wo + kWaves * 16 * kRowPad;  // [kR] m (ln units), [kR] L, [kWaves][kR] weights
+  const int nhalf = pair ? 2 : 1;
+  for (int half = 0; half < nhalf; ++half) {
+    if (tid < kWaves * kG) {
+      // thread (wave ww, head hh); the max and the weighted sum run over ww
+      // (lane bits 3..) with lane exchanges, no serial loop
+      const int hh = tid % kG, ww = tid / kG, r = hh + 8 * half;
+      const float mw = wm[ww * kR + r];
+      float mm = mw;
 #pragma unroll
-    for (int x = kG; x < kWaves * kG; x <<= 1) mm = fmaxf(mm, xor_f(mm, x));
-    const float wt = (mm == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - mm);
-    float L = wt * wm[kWaves * kG + ww * kG + hh];
+      for (int x = kG; x < kWaves * kG; x <<= 1) mm = fmaxf(mm, xor_f(mm, x));
+      const float wt = (mm == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - mm);
+      float L = wt * wm[kWaves * kR + ww * kR + r];
 #pragma unroll
-    for (int x = kG; x < kWaves * kG; x <<= 1) L += xor_f(L, x);
-    ms[2 * kG + ww * kG + hh] = wt;
-    if (ww == 0) {
-      ms[hh] = (mm == -INFINITY) ? -INFINITY : mm * 0.6931471805599453f;  // log2 -> ln units
-      ms[kG + hh] = L;
+      for (int x = kG; x < kWaves * kG; x <<= 1) L += xor_f(L, x);
+      ms[2 * kR + ww * kR + r] = wt;
+      if (ww == 0) {
+        ms[r] = (mm == -INFINITY) ? -INFINITY : mm * 0.6931471805599453f;  // log2 -> ln units
+        ms[kR + r] = L;
+      }
     }
   }
   __syncthreads();
 
-  const int64_t qoff = ((int64_t)tok * a.n_head + h0) * kHD;
-  const int64_t hrow = (int64_t)tok * a.n_head + h0;
-  for (int i = tid; i < G * kHD / 4; i += kThreads) {
-    const int hh = i / (kHD / 4), d = 4 * (i - hh * (kHD / 4));
+  // output rows: (token tr, head hh) in MFMA row r = hh + 8 tr
+  const int nrow = pair ? ntc * G : G;
+  for (int i = tid; i < nrow * kHD / 4; i += kThreads) {
+    const int ri = i / (kHD / 4), d = 4 * (i - ri * (kHD / 4));
+    const int tr = pair ? ri / G : 0, hh = ri - tr * G, r = hh + 8 * tr;
     floatx4 acc4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww)
-      acc4 += ms[2 * kG + ww * kG + hh] * (*(const floatx4 *)(wo + (ww * 16 + hh) * kRowPad + d) +
-                                           *(const floatx4 *)(wo + (ww * 16 + hh + 8) * kRowPad + d));
+    for (int ww = 0; ww < kWaves; ++ww) {
+      floatx4 ov = *(const floatx4 *)(wo + (ww * 16 + r) * kRowPad + d);
+      if (!pair) ov += *(const floatx4 *)(wo + (ww * 16 + hh + 8) * kRowPad + d);
+      acc4 += ms[2 * kR + ww * kR + r] * ov;
+    }
+    const int64_t hrow_r = (int64_t)(tok + tr) * a.n_head + h0 + hh;
     if (a.n_splits == 1) {
-      const float L = ms[kG + hh];
-      const float inv = (ms[hh] == -INFINITY) ? 0.0f : ((L > 0.0f) ? 1.0f / L : 0.0f);
+      const float L = ms[kR + r];
+      const float inv = (ms[r] == -INFINITY) ? 0.0f : ((L > 0.0f) ? 1.0f / L : 0.0f);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         float o1 = acc4[k] * inv;
-        const int64_t oi = qoff + hh * kHD + d + k;
+        const int64_t oi = hrow_r * kHD + d + k;
         if (a.gate) {
           const float sg = sigmoid_dev(a.gate[oi]);
           a.gate[oi] = sg;
@@ -888,18 +932,19 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         a.out[oi] = o1;
       }
     } else {
-      *(floatx4 *)(rec_acc(a, hrow + hh, s) + d) = acc4;
+      *(floatx4 *)(rec_acc(a, hrow_r, s) + d) = acc4;
     }
   }
   RD4_TP();
   if (a.n_splits == 1) return;
-  if (tid < G) {
-    float *ml = rec_ml(a, hrow + tid, s);
-    ml[0] = ms[tid];
-    ml[1] = ms[kG + tid];
+  if (tid < nrow) {
+    const int tr = pair ? tid / G : 0, hh = tid - tr * G, r = hh + 8 * tr;
+    float *ml = rec_ml(a, (int64_t)(tok + tr) * a.n_head + h0 + hh, s);
+    ml[0] = ms[r];
+    ml[1] = ms[kR + r];
   }
-  int *flag = (int *)(ms + 2 * kG + kWaves * kG);
-  if (a.ext_merge || (a.dbg & 1)) return;
+  int *flag = (int *)(ms + 2 * kR + kWaves * kR);
+  if (pair || a.ext_merge || (a.dbg & 1)) return;
   split_tail<kThreads>(a, tok, kvh, hc, h0, G, s, flag, (float *)(flag + 4),
                        (float *)(flag + 4) + kGMaxMerge * kMergeFan);
 }
@@ -912,17 +957,23 @@ size_t decode_lds() {
   // query rows (later the shared fragments and the q4_1 block sums)
   const size_t qreg = (size_t)kG * (kHD * 4 + 16) + 256;
   const size_t tiles = (size_t)TS::WAVES * (TS::R * TS::TB + TS::DT) + qreg;
-  const size_t merge = (2 * TS::WAVES * kG + TS::WAVES * 16 * kRowPad + 2 * kG + TS::WAVES * kG + 4) * 4 +
+  const size_t merge = (2 * TS::WAVES * 16 + TS::WAVES * 16 * kRowPad + 2 * 16 + TS::WAVES * 16 + 4) * 4 +
                        (kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
   return tiles > merge ? tiles : merge;
 }
 
-template <int KT, int VT>
+template <int KT, int VT, bool PAIR = false>
 hipError_t launch(const AttnArgs &a, int n_tok, hipStream_t st) {
   dim3 grid((unsigned)a.n_splits, (unsigned)(a.n_head_kv * a.n_chunks), (unsigned)n_tok);
-  hipLaunchKernelGGL((decode_mfma_kernel<KT, VT>), grid, dim3(64 * TileShape<KT, VT>::WAVES),
+  hipLaunchKernelGGL((decode_mfma_kernel<KT, VT, PAIR>), grid, dim3(64 * TileShape<KT, VT>::WAVES),
                      (decode_lds<KT, VT>()), st, a);
   return hipGetLastError();
+}
+
+// pair mode is built for the cache types a verify step is likely to use
+bool pair_type(int kt, int vt) {
+  return (kt == vt && (kt == F16 || kt == Q8_0 || kt == Q4_0 || kt == Q5_0 || kt == Q4_1)) ||
+         (kt == Q5_0 && vt == Q4_1);
 }
 
 bool hot_k(int t) { return t == F16 || t == Q8_0 || t == Q4_0 || t == Q5_0 || t == Q4_1; }
@@ -936,6 +987,8 @@ bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_d
   return hot_k(kt) && hot_v(vt) && head_dim == kHD && n_head_kv > 0 &&
          n_head % n_head_kv == 0;
 }
+
+bool decode_mfma_pairs(int kt, int vt) { return !RD4_DEC_PV_HILO && pair_type(kt, vt); }
 
 bool decode_mfma_ext_merge() {
   // Split records are merged by a second, short launch: a kernel boundary makes
@@ -952,10 +1005,22 @@ bool decode_mfma_ext_merge() {
 hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hipStream_t st) {
   AttnArgs a = a0;
   a.n_chunks = (a.n_head / a.n_head_kv + kG - 1) / kG;
-  a.ext_merge = (a.n_splits > 1 && decode_mfma_ext_merge()) ? 1 : 0;
+  a.n_tok = n_tok;
+  // pair mode needs host positions, f32 queries, no fused append and one head
+  // chunk per kv head (the rows of two tokens share one 16-row tile)
+  if (a.tok_pair && (a.pos || a.k_new || a.q_f16 || a.n_chunks != 1 || n_tok < 2 ||
+                     RD4_DEC_PV_HILO || !pair_type(kt, vt)))
+    a.tok_pair = 0;
+  a.ext_merge = (a.n_splits > 1 && (a.tok_pair || decode_mfma_ext_merge())) ? 1 : 0;
+  const int grid_tok = a.tok_pair ? (n_tok + 1) / 2 : n_tok;
   hipError_t err = hipErrorInvalidValue;
 #define RD4_D(K, V) \
-  if (kt == K && vt == V) err = launch<K, V>(a, n_tok, st);
+  if (kt == K && vt == V && !a.tok_pair) err = launch<K, V>(a, grid_tok, st);
+#define RD4_P(K, V) \
+  if (kt == K && vt == V && a.tok_pair) err = launch<K, V, true>(a, grid_tok, st);
+  RD4_P(F16, F16) RD4_P(Q8_0, Q8_0) RD4_P(Q4_0, Q4_0) RD4_P(Q5_0, Q5_0) RD4_P(Q4_1, Q4_1)
+  RD4_P(Q5_0, Q4_1)
+#undef RD4_P
   RD4_D(F16, F16) RD4_D(F16, Q8_0) RD4_D(F16, Q4_0)
   RD4_D(Q8_0, F16) RD4_D(Q8_0, Q8_0) RD4_D(Q8_0, Q4_0)
   RD4_D(Q4_0, F16) RD4_D(Q4_0, Q8_0) RD4_D(Q4_0, Q4_0)

@@ -30,6 +30,10 @@ struct AttnArgs {
   int n_chunks;
   int k_lds_stride, v_lds_stride;
   int ext_merge;  // 1: the kernel only writes level-0 records; merge_splits_launch merges
+  // MFMA decode only: 1 = each CTA carries two consecutive tokens (query rows
+  // 0-7 the first token's heads, 8-15 the second's, f16 queries), positions
+  // t + token; n_tok is the token count of the launch
+  int tok_pair, n_tok;
   // Profiling knob (env RD4_DECODE_DBG, 0 in production), MFMA decode kernel:
   // 1 skip the split merge, 2 skip the QK product, 4 skip the PV product,
   // 32 no key tiles, 2048 no tile loads (compute on stale LDS).

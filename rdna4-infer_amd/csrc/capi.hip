@@ -111,7 +111,7 @@ int auto_splits(int keys, int ctas_per_split, int target, int min_keys) {
 int run_attn(const float *q, const void *k, const void *v, float *out, float *gate,
              const int *pos, int t, int n_tok, int n_head, int n_head_kv, int head_dim,
              float scale, int kt, int vt, int splits, hipStream_t st,
-             const float *k_new = nullptr, const float *v_new = nullptr) {
+             const float *k_new = nullptr, const float *v_new = nullptr, int tok_pair = 0) {
   int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
   if (rc) return rc;
   if (n_tok < 1) return fail(RD4_EINVAL, "n_tok must be >= 1%s");
@@ -124,7 +124,10 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
     const int min_s = -splits;
     // CTAs per split: every token's (kv head, head chunk) pairs; the keys of
     // the first token bound the split count
-    const int per_split = n_head_kv * n_chunks * n_tok;
+    // (token pairs share a CTA in the MFMA kernel's pair mode)
+    const bool pairs = tok_pair && mfma && decode_mfma_pairs(kt, vt) && n_chunks == 1 && n_tok >= 2 &&
+                       !pos && !k_new;
+    const int per_split = n_head_kv * n_chunks * (pairs ? (n_tok + 1) / 2 : n_tok);
     splits = mfma ? auto_splits(t + 1, per_split, 256, 64) : auto_splits(t + 1, per_split, 1024, 64);
     if (splits < min_s) splits = min_s;
   }
@@ -144,6 +147,7 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   a.n_head_kv = n_head_kv;
   a.head_dim = head_dim;
   a.scale = scale;
+  a.tok_pair = tok_pair;
   if (splits > 1) {
     Scratch *s = nullptr;
     if ((rc = get_scratch(&s))) return rc;
@@ -307,7 +311,7 @@ int rd4_attn_decode_tokens(const float *q, const void *k, const void *v, float *
   if (n_splits < 0 || n_tok < 1 || t0 < 0)
     return fail(RD4_EINVAL, "need n_tok >= 1, t0 >= 0 and n_splits >= 0%s");
   return run_attn(q, k, v, out, gate, nullptr, t0, n_tok, n_head, n_head_kv, head_dim, scale, kt,
-                  vt, n_splits, (hipStream_t)stream);
+                  vt, n_splits, (hipStream_t)stream, nullptr, nullptr, /*tok_pair=*/1);
 }
 
 int rd4_attn_launch(const float *q, const void *k, const void *v, float *out, int t, int n_head,

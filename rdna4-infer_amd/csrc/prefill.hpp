@@ -26,6 +26,8 @@ hipError_t prefill_mfma_launch(const PrefillArgs &p, hipStream_t st);
 
 bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim);
 hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a, int n_tok, hipStream_t st);
+// True when multi-token decode of this cache pair can put two tokens in a CTA.
+bool decode_mfma_pairs(int kt, int vt);
 // True when split records are merged by a second launch (not the in-kernel tree).
 bool decode_mfma_ext_merge();
 

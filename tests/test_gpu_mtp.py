@@ -5,9 +5,10 @@ decode.
 
 The reference's batched split kernel is bit-identical to its per-token split
 kernel (same key assignment and merge order, graph.cuh:1486-1493). The same
-holds here: rd4_attn_split_batch_launch and rd4_attn_decode_tokens with a given
-split count give each token exactly the bytes of a single-token rd4_attn_decode
-with that split count.
+holds here for rd4_attn_split_batch_launch: with a given split count each token
+gets exactly the bytes of a single-token rd4_attn_decode. rd4_attn_decode_tokens
+reads each K/V tile once for two tokens (f16 queries) and is held to the
+attention tolerance.
 """
 import numpy as np
 import pytest
@@ -37,10 +38,14 @@ def _per_token(rd4, torch, dev, qd, kd, vd, t0, n_tok, kt, vt, splits):
 
 
 @pytest.mark.parametrize("kt,vt", [(2, 2), (1, 1), (4, 5), (3, 3), (0, 2)])
-@pytest.mark.parametrize("n_tok", [2, 4])
-def test_tokens_bit_identical_to_per_token(rd4, orc, dev, kt, vt, n_tok):
+@pytest.mark.parametrize("n_tok", [2, 3, 4])
+def test_tokens_vs_per_token_and_oracle(rd4, orc, dev, kt, vt, n_tok):
+    """Split-batch (the reference entry) is bit-identical to per-token decode at
+    the same split count. rd4_attn_decode_tokens may put two tokens in one CTA
+    with f16 queries (pair mode), so it is held to the tolerance instead, against
+    per-token decode and the oracle; odd n_tok leaves the last pair half full."""
     import torch
-    print("mtp bit-identity kt=%d vt=%d n_tok=%d" % (kt, vt, n_tok), flush=True)
+    print("mtp kt=%d vt=%d n_tok=%d" % (kt, vt, n_tok), flush=True)
     n = 3000
     k, v, kd, vd = _caches(orc, torch, dev, kt, vt, n, 300 + kt)
     t0 = n - n_tok
@@ -48,20 +53,40 @@ def test_tokens_bit_identical_to_per_token(rd4, orc, dev, kt, vt, n_tok):
     qd = to_dev(q, torch, dev)
     splits = 6
     want = _per_token(rd4, torch, dev, qd, kd, vd, t0, n_tok, kt, vt, splits)
-    out = torch.empty_like(qd)
-    rd4.attn_decode_tokens(qd, kd, vd, out, t0, n_tok, NH, NKV, HD, 1 / 16, kt, vt, n_splits=splits)
     pos = to_dev(np.arange(t0, n, dtype=np.int32), torch, dev)
     out2 = torch.empty_like(qd)
     rd4.attn_split_batch(qd, kd, vd, out2, pos, NH, NKV, HD, 1 / 16, kt, vt, splits)
+    out = torch.empty_like(qd)
+    rd4.attn_decode_tokens(qd, kd, vd, out, t0, n_tok, NH, NKV, HD, 1 / 16, kt, vt, n_splits=splits)
     torch.cuda.synchronize()
-    assert np.array_equal(out.cpu().numpy(), want)
     assert np.array_equal(out2.cpu().numpy(), want)
-    # and the automatic split count against the oracle
-    rd4.attn_decode_tokens(qd, kd, vd, out, t0, n_tok, NH, NKV, HD, 1 / 16, kt, vt)
-    torch.cuda.synchronize()
+    check_close(out.cpu().numpy(), want, "tokens vs per-token")
     ref = orc.attn_batch(q.reshape(n_tok, NH, HD), k, v, np.arange(t0, n, dtype=np.int32), NH, NKV,
                          HD, 1 / 16, kt, vt, threads=8)
+    check_close(out.cpu().numpy(), ref, "tokens forced splits")
+    rd4.attn_decode_tokens(qd, kd, vd, out, t0, n_tok, NH, NKV, HD, 1 / 16, kt, vt)
+    torch.cuda.synchronize()
     check_close(out.cpu().numpy(), ref, "tokens auto")
+
+
+@pytest.mark.parametrize("kt,vt", [(2, 2), (1, 1)])
+def test_tokens_split_with_only_the_last_key(rd4, orc, dev, kt, vt):
+    """3009 keys in 189 splits of 16: the last split holds key 3008 only, which
+    the first token of the pair (position 3007) must not see: its rows in that
+    split have no key at all and must merge as empty."""
+    import torch
+    n, n_tok = 3009, 2
+    k, v, kd, vd = _caches(orc, torch, dev, kt, vt, n, 320 + kt)
+    q = orc.randn(n_tok * NH * HD, 330)
+    out = torch.empty(n_tok * NH * HD, device=dev)
+    rd4.attn_decode_tokens(to_dev(q, torch, dev), kd, vd, out, n - n_tok, n_tok, NH, NKV, HD, 1 / 16,
+                           kt, vt, n_splits=189)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    ref = orc.attn_batch(q.reshape(n_tok, NH, HD), k, v, np.arange(n - n_tok, n, dtype=np.int32), NH,
+                         NKV, HD, 1 / 16, kt, vt, threads=8)
+    check_close(got, ref, "last-key split")
 
 
 @pytest.mark.parametrize("kt,vt", [(2, 2), (4, 5)])
@@ -131,3 +156,45 @@ def test_tokens_rejects_bad_arguments(rd4, dev):
     for t0, n_tok, splits in ((-1, 1, 0), (0, 0, 0), (5, 1, -1)):
         with pytest.raises(rd4.Rd4Error):
             rd4.attn_decode_tokens(x, c, c, x, t0, n_tok, NH, NKV, HD, 1 / 16, 1, 1, n_splits=splits)
+
+
+@pytest.mark.parametrize("kt,vt", [(2, 2), (4, 5)])
+def test_layer_verify_step_epilogue_then_tokens(rd4, orc, dev, kt, vt):
+    """One full-attention layer of an MTP verify step, as graph.cuh:1444-1535
+    runs it for a chunk: the fused epilogue writes q, the gate and the chunk's K/V
+    rows, then the multi-token decode attends and gates. Checked against the
+    oracle doing the same steps (deinterleave, RMSNorm, RoPE, quantize, f64
+    attention, gate)."""
+    import torch
+    n0, n_tok, n_rot, eps, base = 1500, 4, 64, 1e-6, 10000000.0
+    n = n0 + n_tok
+    k, v, kd, vd = _caches(orc, torch, dev, kt, vt, n, 400)
+    krb, vrb = orc.row_bytes(kt, HD), orc.row_bytes(vt, HD)
+    qg = (orc.randn(n_tok * NH * 2 * HD, 410) * 2).astype(np.float32)
+    kn = (orc.randn(n_tok * NKV * HD, 411) * 2).astype(np.float32)
+    vn = orc.randn(n_tok * NKV * HD, 412).astype(np.float32)
+    qw = (1 + 0.1 * orc.randn(HD, 413)).astype(np.float32)
+    kw = (1 + 0.1 * orc.randn(HD, 414)).astype(np.float32)
+    pos = np.arange(n0, n, dtype=np.int32)
+    q_out = torch.empty(n_tok * NH * HD, device=dev)
+    g_out = torch.empty_like(q_out)
+    k_out = torch.empty(n_tok * NKV * HD, device=dev)
+    rd4.qk_norm_rope_append(to_dev(qg, torch, dev), to_dev(kn, torch, dev), to_dev(vn, torch, dev),
+                            to_dev(qw, torch, dev), to_dev(kw, torch, dev), eps, n_rot, base,
+                            to_dev(pos, torch, dev), n_tok, NH, NKV, HD, q_out, kd, vd, kt, vt,
+                            gate_out=g_out, k_out=k_out)
+    out = torch.empty_like(q_out)
+    rd4.attn_decode_tokens(q_out, kd, vd, out, n0, n_tok, NH, NKV, HD, 1 / 16, kt, vt, gate=g_out)
+    torch.cuda.synchronize()
+    # oracle pipeline on the host
+    q3 = qg.reshape(n_tok, NH, 2, HD)
+    q_ref = orc.rope(orc.rms_norm(q3[:, :, 0].ravel(), qw, HD, eps), n_tok, NH, HD, n_rot, base, pos)
+    k_ref = orc.rope(orc.rms_norm(kn, kw, HD, eps), n_tok, NKV, HD, n_rot, base, pos).ravel()
+    kc, vc = k.copy(), v.copy()
+    kc[n0 * NKV * krb:] = orc.store_rows(kt, k_out.cpu().numpy())  # the GPU's own rows (bit-checked elsewhere)
+    vc[n0 * NKV * vrb:] = orc.store_rows(vt, vn)
+    assert np.array_equal(kd.cpu().numpy(), kc) and np.array_equal(vd.cpu().numpy(), vc)
+    assert np.abs(k_out.cpu().numpy() - k_ref).max() < 1e-3
+    att = orc.attn_batch(q_ref.reshape(n_tok, NH, HD), kc, vc, pos, NH, NKV, HD, 1 / 16, kt, vt, threads=8)
+    _, want = orc.sigmoid_gate(q3[:, :, 1].ravel(), att.ravel())
+    check_close(out.cpu().numpy(), want, "layer verify step")
