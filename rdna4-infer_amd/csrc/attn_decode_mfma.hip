@@ -46,6 +46,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #ifndef RD4_DEC_TRACE
 #define RD4_DEC_TRACE 0
 #endif
+#ifndef RD4_DEC_ASM_WAIT
+#define RD4_DEC_ASM_WAIT 0
+#endif
 #ifndef RD4_DEC_AUX
 #define RD4_DEC_AUX 0
 #endif
@@ -65,7 +68,13 @@ __device__ __forceinline__ void wave_sync() {
 // (loads complete in issue order); also a compiler memory barrier.
 template <int N>
 __device__ __forceinline__ void wait_vm() {
+#if RD4_DEC_ASM_WAIT
   __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+#else
+  // the builtin (not asm) lets the compiler's wait-count tracking see the wait
+  static_assert(N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+#endif
 }
 
 template <int T>
@@ -334,6 +343,28 @@ __device__ __forceinline__ uint32_t split_prod2(float p0, float d0, float p1, fl
 #ifndef RD4_DEC_PV_HILO
 #define RD4_DEC_PV_HILO 0
 #endif
+// The 8 per-block float4 entries p[16 b .. 16 b + 3] of a per-tile scale table,
+// read with one asm block that waits for its own LDS reads. Through ordinary
+// loads the compiler places a vmcnt(0) before them (it cannot rule out that the
+// tile DMA still in flight writes the table), which would stall every tile on
+// the next tile's prefetch.
+__device__ __forceinline__ void tbl_read8(const float *p, floatx4 (&out)[8]) {
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)p;
+  __asm__ volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %8 offset:64\n\t"
+      "ds_read_b128 %2, %8 offset:128\n\t"
+      "ds_read_b128 %3, %8 offset:192\n\t"
+      "ds_read_b128 %4, %8 offset:256\n\t"
+      "ds_read_b128 %5, %8 offset:320\n\t"
+      "ds_read_b128 %6, %8 offset:384\n\t"
+      "ds_read_b128 %7, %8 offset:448\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(out[4]), "=&v"(out[5]),
+        "=&v"(out[6]), "=&v"(out[7])
+      : "v"(a)
+      : "memory");
+}
 // f16 of four products in the rows n < 8 (lo_mask = 0 there) and zero in the
 // rows n >= 8, as the B operand of one PV MFMA.
 __device__ __forceinline__ half4 hi_only4(float x0, float x1, float x2, float x3, uint32_t lo_mask) {
@@ -425,13 +456,18 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   }
 
   // ---- async tile ring: stage i of this wave at ring + (i % R) * TB
-  uint8_t *ring = smem + w * (R * TB + DT);
+  uint8_t *ring = smem + w * (R * TB);
   // tables [8 blocks][16 keys]: K scales, V scales, K offsets, V offsets
   constexpr int iDK = KT != F16 ? 0 : -1;
   constexpr int iDV = VT != F16 ? (KT != F16) : -1;
   constexpr int iMK = KT == Q4_1 ? (KT != F16) + (VT != F16) : -1;
   constexpr int iMV = VT == Q4_1 ? (KT != F16) + (VT != F16) + (KT == Q4_1) : -1;
-  float *dk_t = (float *)(ring + R * TB);
+  // The scale tables live in their own static LDS array: a separate object from
+  // the DMA ring, so the compiler can prove their reads do not alias tile loads
+  // still in flight and inserts no vmcnt(0) wait (which would stall on the
+  // next tile's prefetch) before them.
+  __shared__ __align__(16) float tbl_s[kWaves][DT > 0 ? DT / 4 : 4];
+  float *dk_t = tbl_s[w];
   float *dv_t = dk_t + 128 * (iDV > 0 ? iDV : 0);
   float *mk_t = dk_t + 128 * (iMK > 0 ? iMK : 0);
   float *mv_t = dk_t + 128 * (iMV > 0 ? iMV : 0);
@@ -495,7 +531,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   // global->LDS DMA, issued before any tile so they are not queued behind the
   // tiles; rows are padded by 16 bytes so the per-row fragment reads below do
   // not collide in one bank.
-  uint8_t *q_lds = smem + kWaves * (R * TB + DT);
+  uint8_t *q_lds = smem + kWaves * (R * TB);
   const int qcw = a.q_f16 ? kHD / 8 : kHD / 4;  // 16-byte chunks per query row
   const int qsb = 16 * (qcw + 1);               // padded row stride in bytes
   auto issue_q = [&]() {  // one load instruction per 64 chunks, spread over the waves
@@ -668,17 +704,20 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         for (int b = 0; b < 8; ++b)
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), qf[b], acc, 0, 0, 0);
       } else {
+        floatx4 dks[8], mks[KT == Q4_1 ? 8 : 1];
+        tbl_read8(dk_t + 4 * g, dks);
+        if constexpr (KT == Q4_1) tbl_read8(mk_t + 4 * g, mks);
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
           const floatx4 z = {0.f, 0.f, 0.f, 0.f};
           const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), qf[b], z, 0, 0, 0);
-          const float4 dk = *(const float4 *)(dk_t + b * 16 + 4 * g);
+          const float4 dk = make_float4(dks[b][0], dks[b][1], dks[b][2], dks[b][3]);
           acc[0] = fmaf(dk.x, c[0], acc[0]);
           acc[1] = fmaf(dk.y, c[1], acc[1]);
           acc[2] = fmaf(dk.z, c[2], acc[2]);
           acc[3] = fmaf(dk.w, c[3], acc[3]);
           if constexpr (KT == Q4_1) {
-            const float4 mk = *(const float4 *)(mk_t + b * 16 + 4 * g);
+            const float4 mk = make_float4(mks[b][0], mks[b][1], mks[b][2], mks[b][3]);
             acc[0] = fmaf(mk.x, qblk[b], acc[0]);
             acc[1] = fmaf(mk.y, qblk[b], acc[1]);
             acc[2] = fmaf(mk.z, qblk[b], acc[2]);
@@ -764,9 +803,12 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         }
       }
     } else {
+      floatx4 dvs[8], mvs[VT == Q4_1 ? 8 : 1];
+      tbl_read8(dv_t + 4 * g, dvs);
+      if constexpr (VT == Q4_1) tbl_read8(mv_t + 4 * g, mvs);
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
-        const float4 dv = *(const float4 *)(dv_t + b * 16 + 4 * g);
+        const float4 dv = make_float4(dvs[b][0], dvs[b][1], dvs[b][2], dvs[b][3]);
 #if RD4_DEC_PV_HILO
         const half4 pf = __builtin_bit_cast(
             half4, u32x2{split_prod2(sc[0], dv.x, sc[1], dv.y, lo_mask),
@@ -777,7 +819,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
 #endif
         if constexpr (VT == Q4_1) {
           if (pair || n < 8) {
-            const float4 mv = *(const float4 *)(mv_t + b * 16 + 4 * g);
+            const float4 mv = make_float4(mvs[b][0], mvs[b][1], mvs[b][2], mvs[b][3]);
             cm[b] = fmaf(sc[0], mv.x, fmaf(sc[1], mv.y, fmaf(sc[2], mv.z, fmaf(sc[3], mv.w, cm[b]))));
           }
         }
@@ -956,7 +998,7 @@ size_t decode_lds() {
   using TS = TileShape<KT, VT>;
   // query rows (later the shared fragments and the q4_1 block sums)
   const size_t qreg = (size_t)kG * (kHD * 4 + 16) + 256;
-  const size_t tiles = (size_t)TS::WAVES * (TS::R * TS::TB + TS::DT) + qreg;
+  const size_t tiles = (size_t)TS::WAVES * TS::R * TS::TB + qreg;  // scale tables are static LDS
   const size_t merge = (2 * TS::WAVES * 16 + TS::WAVES * 16 * kRowPad + 2 * 16 + TS::WAVES * 16 + 4) * 4 +
                        (kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
   return tiles > merge ? tiles : merge;
