@@ -120,6 +120,14 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   const int64_t rec = 2 + head_dim;
   const bool aligned16 = ((((uintptr_t)k) | ((uintptr_t)v) | ((uintptr_t)q)) & 15) == 0;
   const bool mfma = aligned16 && decode_mfma_supported(kt, vt, n_head, n_head_kv, head_dim);
+  // RD_ATTN_SPLITS (graph.cuh:509-519): a forced split count for the automatic
+  // and minimum-count launches, so the reference's split-vs-unsplit checks
+  // (RD_ATTN_SPLITS=1 = one split) mean what they meant.
+  static const int env_splits = [] {
+    const char *e = std::getenv("RD_ATTN_SPLITS");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (splits <= 0 && env_splits > 0) splits = env_splits > kMaxSplits ? kMaxSplits : env_splits;
   if (splits <= 0) {  // automatic, at least -splits
     const int min_s = -splits;
     // CTAs per split: every token's (kv head, head chunk) pairs; the keys of

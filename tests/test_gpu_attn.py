@@ -235,3 +235,46 @@ def test_baseline_decode_configs_full_size(rd4, orc, dev, cfg):
     torch.cuda.synchronize()
     _, want = orc.sigmoid_gate(g, orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, kt, vt, threads=8).ravel())
     check_close(out.cpu().numpy(), want, cfg)
+
+
+def test_rd_attn_splits_env_forces_the_count():
+    """RD_ATTN_SPLITS=N (graph.cuh:509-519) forces N splits on the launches that
+    pick their own count: attn_launch / attn_launch_split then equal a forced
+    rd4_attn_decode(n_splits=N) bit for bit. Run in a child process, since the
+    library reads the variable once."""
+    import subprocess
+    import sys
+    code = r'''
+import sys
+sys.path.insert(0, "tests"); sys.path.insert(0, "oracle")
+import numpy as np, torch
+from conftest import load_package
+import oracle as orc
+from test_gpu_attn import make_cache
+from gpu_util import to_dev
+rd4 = load_package(); dev = torch.device("cuda:0")
+nh, nkv, hd, n = 24, 4, 256, 5000
+k = to_dev(make_cache(orc, 2, n, nkv, hd, 500), torch, dev)
+v = to_dev(make_cache(orc, 2, n, nkv, hd, 501), torch, dev)
+q = to_dev(orc.randn(nh * hd, 502), torch, dev)
+outs = []
+for f in ("launch", "split", "forced"):
+    o = torch.empty(nh * hd, device=dev)
+    if f == "launch":
+        rd4.attn_launch(q, k, v, o, n - 1, nh, nkv, hd, 1 / 16, 2, 2)
+    elif f == "split":
+        rd4.attn_launch_split(q, k, v, o, o, n - 1, nh, nkv, hd, 1 / 16, 2, 2, 4)
+    else:
+        rd4.attn_decode(q, k, v, o, n - 1, nh, nkv, hd, 1 / 16, 2, 2, n_splits=int(sys.argv[1]))
+    torch.cuda.synchronize()
+    outs.append(o.cpu().numpy())
+assert np.array_equal(outs[0], outs[2]) and np.array_equal(outs[1], outs[2]), "env count not used"
+print("ok")
+'''
+    import os
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for count in ("1", "3"):
+        env = dict(os.environ, RD_ATTN_SPLITS=count)
+        r = subprocess.run([sys.executable, "-c", code, count], cwd=root, env=env,
+                           capture_output=True, text=True, timeout=180)
+        assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
