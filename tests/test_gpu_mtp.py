@@ -198,3 +198,29 @@ def test_layer_verify_step_epilogue_then_tokens(rd4, orc, dev, kt, vt):
     att = orc.attn_batch(q_ref.reshape(n_tok, NH, HD), kc, vc, pos, NH, NKV, HD, 1 / 16, kt, vt, threads=8)
     _, want = orc.sigmoid_gate(q3[:, :, 1].ravel(), att.ravel())
     check_close(out.cpu().numpy(), want, "layer verify step")
+
+
+def test_tokens_wide_group_takes_per_token_ctas(rd4, orc, dev):
+    """GQA group 16 (two head chunks per kv head) cannot pair tokens in one
+    16-row tile; the multi-token entry then runs one token per CTA and stays
+    bit-identical to per-token decode at the same split count."""
+    import torch
+    nh, nkv, n, n_tok = 32, 2, 1200, 3
+    k = make_cache(orc, 3, n, nkv, HD, 700)
+    v = make_cache(orc, 3, n, nkv, HD, 701)
+    kd, vd = to_dev(k, torch, dev), to_dev(v, torch, dev)
+    q = orc.randn(n_tok * nh * HD, 702)
+    qd = to_dev(q, torch, dev)
+    out = torch.empty_like(qd)
+    rd4.attn_decode_tokens(qd, kd, vd, out, n - n_tok, n_tok, nh, nkv, HD, 1 / 16, 3, 3, n_splits=5)
+    per = []
+    for i in range(n_tok):
+        o = torch.empty(nh * HD, device=dev)
+        rd4.attn_decode(qd[i * nh * HD:(i + 1) * nh * HD].clone(), kd, vd, o, n - n_tok + i, nh, nkv, HD,
+                        1 / 16, 3, 3, n_splits=5)
+        per.append(o)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), torch.cat(per).cpu().numpy())
+    ref = orc.attn_batch(q.reshape(n_tok, nh, HD), k, v, np.arange(n - n_tok, n, dtype=np.int32), nh, nkv,
+                         HD, 1 / 16, 3, 3, threads=8)
+    check_close(out.cpu().numpy(), ref, "wide group")
