@@ -6,13 +6,13 @@
 // nn.cuh:405-412 and the append of graph.cuh:1011-1031 optionally fused:
 // out[h] = softmax_j(q_h . k_j * scale) . V over keys 0..t, f32 accumulation.
 //
-// Work decomposition: CTA = 8 waves = one (token, kv head, <=8-query-head
-// chunk, key split). Each wave walks its own 16-key tiles of the split
-// (tiles w, w+8, ...: the 8 waves stream adjacent memory) with a private
+// Work decomposition: CTA = 8 waves (4 for wide tiles) = one (token, kv head,
+// <=8-query-head chunk, key split). Each wave walks its own 16-key tiles of the
+// split (tiles w, w+8, ...: the waves stream adjacent memory) with a private
 // online-softmax state, so the main loop has no CTA barrier. Per tile:
-//   1. the tile's raw K and V rows (exactly the cache bytes) arrive with
-//      16-byte global loads issued one tile ahead into registers, and are
-//      written to a wave-private LDS buffer;
+//   1. the tile's raw K and V rows (exactly the cache bytes) arrive by
+//      global->LDS DMA (16 bytes per lane) into a wave-private ring, issued
+//      ahead of use; the per-block scales (and q4_1 offsets) become f32 tables;
 //   2. S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K
 //      converted to f16 on the fly (f16 as is; the quantized types' integers,
 //      exact in f16), B = the query rows. The 16 MFMA rows carry the group's
@@ -22,13 +22,15 @@
 //      m * sum(q over the block), the block sums formed once per CTA;
 //   3. online softmax in registers (exp2 domain); the C layout of S^T gives each
 //      lane one query row x 4 keys, exactly the B operand layout PV needs; the
-//      O rescale is skipped when no row's running max moved;
+//      running max moves only by more than 2^8, so O is rarely rescaled;
 //   4. O^T += V^T P^T on v_mfma_f32_16x16x16_f16: A = 16 dims x 16 keys of V
-//      read from LDS, B = p (hi/lo rows again), with the quantized V's d folded
-//      into p per 32-dim block; q4_1's offsets contribute sum_j p_j m_j per
-//      block, kept in f32 registers and added to the block's dims at the end.
-// The 4 waves' states merge through LDS into one (m, l, acc) record per query
-// head; splits merge through the two-level tree of merge.hpp in the same launch.
+//      read from LDS, B = f16(p * d) in the head rows (d = the quantized V's
+//      per-block scale); q4_1's offsets contribute sum_j p_j m_j per block, kept
+//      in f32 registers and added to the block's dims at the end.
+// The waves' states merge through LDS into one (m, l, acc) record per query
+// head and split; merge_splits_kernel (merge.hip) folds the splits and applies
+// the gate in a second short launch. In pair mode (PAIR) rows 0-7 and 8-15 are
+// the heads of two consecutive tokens with f16 queries, so the tiles serve both.
 #include <cstdlib>
 
 #include "kv_quant.hpp"
