@@ -109,15 +109,16 @@ def decode_workload(torch, rd4, kt, ctx, outlier, gated=True, vt=None):
     attn_bytes = kv_bytes + small + append  # the append is inside the attention launch
     step_bytes = attn_bytes
 
-    def cpu(budget_s=12.0):
-        """Scalar f64 oracle on the same cache, repeated for ~budget_s; returns GB/s."""
+    def cpu(budget_s=12.0, threads=1):
+        """f64 oracle on the same cache, repeated for ~budget_s; returns GB/s. threads > 1
+        runs its OpenMP form (parallel over heads)."""
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as orc
         kh, vh = kc.cpu().numpy(), vc.cpu().numpy()
         qh = q.cpu().numpy()
         reps, t0 = 0, time.perf_counter()
         while True:
-            orc.attn_decode(qh, kh, vh, pos, NH, NKV, HD, scale, kt, vt)
+            orc.attn_decode(qh, kh, vh, pos, NH, NKV, HD, scale, kt, vt, threads=threads)
             reps += 1
             if time.perf_counter() - t0 > budget_s:
                 break
@@ -295,6 +296,12 @@ def main():
         res["cpu_baseline"] = {"value": round(v, 4), "unit": unit, "cores": 1, "kind": "port",
                                "sample": sample + " (oracle/oracle.c, f64 accumulate)",
                                "host_nproc": os.cpu_count()}
+        if not is_prefill:
+            # the optional multi-core form: OpenMP over heads, on the box's CPU share
+            thr = max(1, min(16, os.cpu_count() or 1, NH))
+            v2, sample2 = cpu(budget_s=5.0, threads=thr)
+            res["cpu_baseline_omp"] = {"value": round(v2, 4), "unit": unit, "cores": thr,
+                                       "kind": "port", "sample": sample2}
     if args.extra:
         res["extra"] = {}
         for name in ("decode_f16", "decode_q4_0", "decode_q5_0_q4_1", "decode_tokens", "prefill"):
