@@ -278,3 +278,27 @@ print("ok")
         r = subprocess.run([sys.executable, "-c", code, count], cwd=root, env=env,
                            capture_output=True, text=True, timeout=180)
         assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
+@pytest.mark.parametrize("kt", [1, 2])
+@pytest.mark.parametrize("shift", [20.0, -20.0])
+def test_merge_with_lse_spread(rd4, orc, dev, kt, shift):
+    """The merge audit of bench_attn_gpu.hip:1161-1428: split records whose
+    log-sum-exp maxima differ by about +-20. All heads share one query direction
+    u, and the first 64 keys lean along u, so their scores sit about `shift`
+    above (or below) the other keys'. Forced split counts put those keys in
+    one split or spread them out."""
+    import torch
+    nh, nkv, hd, n = 24, 4, 256, 4096
+    u = orc.randn(hd, 800)
+    u = (u / np.linalg.norm(u)).astype(np.float32)
+    q = np.tile(u * 16.0, nh).astype(np.float32)  # |q| = 16: a unit key along u scores 1.0
+    kx = orc.randn(n * nkv * hd, 801).reshape(n, nkv, hd) * 0.2
+    kx[:64] += (shift * u)[None, None, :]
+    k = orc.store_rows(kt, kx.astype(np.float32).ravel())
+    v = make_cache(orc, kt, n, nkv, hd, 802)
+    want = orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, kt, kt, threads=8)
+    for splits in (1, 4, 64):
+        got, _ = run_decode(rd4, torch, dev, q, k, v, n - 1, nh, nkv, hd, kt, kt, n_splits=splits)
+        check_close(got, want, "shift %g splits %d" % (shift, splits))
+        assert np.all(np.isfinite(got))
