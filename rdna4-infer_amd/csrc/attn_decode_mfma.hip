@@ -48,6 +48,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #ifndef RD4_DEC_TRACE
 #define RD4_DEC_TRACE 0
 #endif
+// profiling knobs (RD4_DECODE_DBG bits 2, 4, 32, 2048 skip the QK product, the PV
+// product, all tiles, all loads); off in production builds, where their
+// branches cost register copies in the tile loop
+#ifndef RD4_DEC_KNOBS
+#define RD4_DEC_KNOBS 0
+#endif
 #ifndef RD4_DEC_ASM_WAIT
 #define RD4_DEC_ASM_WAIT 0
 #endif
@@ -147,28 +153,48 @@ __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const u
 // Dim of head_dim held in k-slot j of lane group g (lanes 16g..16g+15) for the
 // 32-dim block b of the S^T = K Q^T product. Any order within a block is a
 // valid MFMA contraction as long as K and Q use the same one; it is chosen so
-// that every lane reads its K bytes with aligned 32-bit LDS loads. Quantized
-// blocks start 2 bytes past a 4-byte boundary in every other block (34- and
-// 18-byte blocks); there the lane group that would straddle the row's edges
-// takes the block's first two and last two values instead. Pairs (j, j+1)
-// with j even are always two consecutive dims starting at an even dim.
+// that every lane reads its K bytes with aligned 32-bit LDS loads. q8_0 blocks
+// (34 bytes) start 2 bytes past a 4-byte boundary in every other block; there
+// the lane group that would straddle the row's edges takes the block's first
+// two and last two values instead. q4_0 (18-byte blocks) realigns two words.
 template <int KT>
 __host__ __device__ constexpr int k_dim(int b, int g, int j) {
-  // q5_0 / q4_1: low nibbles (g < 2) hold elements 0..15, high nibbles 16..31,
-  // read with aligned words (q4_1) or realigned words (q5_0) in every block
-  if (KT == Q5_0 || KT == Q4_1) return 32 * b + 16 * (g >> 1) + 8 * (g & 1) + j;
-  if (KT == F16 || (b & 1)) {
-    if (KT == Q4_0) return 32 * b + 16 * (g >> 1) + 8 * (g & 1) + j;
-    return 32 * b + 8 * g + j;
-  }
-  if (KT == Q8_0) {
-    if (g < 3) return 32 * b + 8 * g + 2 + j;
-    return 32 * b + (j < 4 ? 26 + j : j == 4 ? 0 : j == 5 ? 1 : j == 6 ? 30 : 31);
-  }
-  // Q4_0: low nibbles (g < 2) hold elements 0..15, high nibbles 16..31
-  const int base = 32 * b + 16 * (g >> 1);
-  if ((g & 1) == 0) return base + 2 + j;
-  return base + (j < 4 ? 10 + j : j == 4 ? 0 : j == 5 ? 1 : j == 6 ? 14 : 15);
+  // q4_0 / q4_1: lane group g converts the 4 quant bytes 4g..4g+3 of the block;
+  // slots 0-3 are the low nibbles of bytes 0, 2, 1, 3 (elements 4g + those),
+  // slots 4-7 the high nibbles (elements 16 + the same)
+  if (KT == Q4_0 || KT == Q4_1) return 32 * b + 4 * g + ((j & 1) << 1) + ((j >> 1) & 1) + 16 * (j >> 2);
+  // q5_0: low nibbles (g < 2) hold elements 0..15, high nibbles 16..31, read
+  // with realigned words in every block
+  if (KT == Q5_0) return 32 * b + 16 * (g >> 1) + 8 * (g & 1) + j;
+  if (KT == F16 || (b & 1)) return 32 * b + 8 * g + j;
+  // Q8_0, even blocks
+  if (g < 3) return 32 * b + 8 * g + 2 + j;
+  return 32 * b + (j < 4 ? 26 + j : j == 4 ? 0 : j == 5 ? 1 : j == 6 ? 30 : 31);
+}
+
+// (x & m) | b in one VALU instruction (the compiler splits it into two
+// literal-operand ops; VOP3 on this target takes no literal, so m comes from
+// an SGPR)
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t b) {
+  uint32_t r;
+  __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(b));
+  return r;
+}
+// Nibbles at bits 0-3 and 16-19 of v -> two f16 of (nibble + bias), bias -8 or 0.
+template <int BIAS>
+__device__ __forceinline__ uint32_t nib_lo_h2(uint32_t v) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 c = {(_Float16)(-1024.0f + BIAS), (_Float16)(-1024.0f + BIAS)};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, and_or(v, 0x000f000fu, 0x64006400u)) + c);
+}
+// Nibbles at bits 4-7 and 20-23 of v: the f16 1024 + 16n, times 1/16 less 64 - bias,
+// is n + bias with no rounding (one packed fma).
+template <int BIAS>
+__device__ __forceinline__ uint32_t nib_hi_h2(uint32_t v) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 sc = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const h2 c = {(_Float16)(-64.0f + BIAS), (_Float16)(-64.0f + BIAS)};
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, and_or(v, 0x00f000f0u, 0x64006400u)), sc, c));
 }
 
 // Bytes (sel-chosen pair) of v -> two f16 holding the same signed integers:
@@ -215,14 +241,24 @@ __device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g, int n
   u32x4 r;
   if constexpr (KT == F16) {
     r = *(const u32x4 *)(krow + 16 * ((4 * b + g) ^ n_of_row));
-  } else if constexpr (KT == Q4_1 || KT == Q5_0) {
+  } else if constexpr (KT == Q4_0 || KT == Q4_1) {
+    // the 4 quant bytes 4g..4g+3; q4_0's are 2 bytes off a word in even blocks
+    constexpr int BB = block_bytes(KT);
+    uint32_t x;
+    if (KT == Q4_1) x = lds_u32(krow + BB * b + 4 + 4 * g);
+    else if (b & 1) x = lds_u32(krow + BB * b + 2 + 4 * g);
+    else x = __builtin_amdgcn_alignbyte(lds_u32(krow + BB * b + 4 + 4 * g), lds_u32(krow + BB * b + 4 * g), 2);
+    constexpr int BIAS = KT == Q4_0 ? -8 : 0;
+    const uint32_t x8 = x >> 8;
+    r[0] = nib_lo_h2<BIAS>(x);
+    r[1] = nib_lo_h2<BIAS>(x8);
+    r[2] = nib_hi_h2<BIAS>(x);
+    r[3] = nib_hi_h2<BIAS>(x8);
+  } else if constexpr (KT == Q5_0) {
     constexpr int BB = block_bytes(KT);
     const int gg = g & 1, sh = (g & 2) ? 4 : 0;
     uint32_t x, y;
-    if constexpr (KT == Q4_1) {  // 20-byte blocks: qs at +4 is word aligned
-      x = lds_u32(krow + BB * b + 4 + 8 * gg);
-      y = lds_u32(krow + BB * b + 8 + 8 * gg);
-    } else if (b & 1) {  // 22-byte blocks: qs at +6 is word aligned in odd blocks
+    if (b & 1) {  // 22-byte blocks: qs at +6 is word aligned in odd blocks
       x = lds_u32(krow + BB * b + 6 + 8 * gg);
       y = lds_u32(krow + BB * b + 10 + 8 * gg);
     } else {
@@ -234,12 +270,7 @@ __device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g, int n
     }
     x >>= sh;
     y >>= sh;
-    if constexpr (KT == Q4_1) {
-      r[0] = unibpair_to_h2(x, 0x0c010c00u);
-      r[1] = unibpair_to_h2(x, 0x0c030c02u);
-      r[2] = unibpair_to_h2(y, 0x0c010c00u);
-      r[3] = unibpair_to_h2(y, 0x0c030c02u);
-    } else {
+    {
       // the block's 32 high bits at +2; this lane's 8 elements are bits
       // 16 * (g >> 1) + 8 * gg ..
       const uint32_t qh = lds_u16(krow + BB * b + 2) | (lds_u16(krow + BB * b + 4) << 16);
@@ -250,30 +281,20 @@ __device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g, int n
       r[3] = q5pair_to_h2(y, 0x0c030c02u, (hb >> 6) & 1u, (hb >> 7) & 1u);
     }
   } else {
+    static_assert(KT == Q8_0, "q8_0 here");
     constexpr int BB = block_bytes(KT);
-    const int gg = KT == Q8_0 ? g : (g & 1);  // q4_0: lane groups g and g^2 read the same bytes
     uint32_t x, y;
     if (b & 1) {
-      x = lds_u32(krow + BB * b + 2 + 8 * gg);
-      y = lds_u32(krow + BB * b + 6 + 8 * gg);
+      x = lds_u32(krow + BB * b + 2 + 8 * g);
+      y = lds_u32(krow + BB * b + 6 + 8 * g);
     } else {
-      x = lds_u32(krow + BB * b + 4 + 8 * gg);
-      y = __builtin_amdgcn_perm(lds_u32(krow + BB * b + 8 + 8 * gg), lds_u32(krow + BB * b), sel_edge);
+      x = lds_u32(krow + BB * b + 4 + 8 * g);
+      y = __builtin_amdgcn_perm(lds_u32(krow + BB * b + 8 + 8 * g), lds_u32(krow + BB * b), sel_edge);
     }
-    if constexpr (KT == Q8_0) {
-      r[0] = i8pair_to_h2(x, 0x0c010c00u);
-      r[1] = i8pair_to_h2(x, 0x0c030c02u);
-      r[2] = i8pair_to_h2(y, 0x0c010c00u);
-      r[3] = i8pair_to_h2(y, 0x0c030c02u);
-    } else {
-      const int sh = (g & 2) ? 4 : 0;
-      x >>= sh;
-      y >>= sh;
-      r[0] = nibpair_to_h2(x, 0x0c010c00u);
-      r[1] = nibpair_to_h2(x, 0x0c030c02u);
-      r[2] = nibpair_to_h2(y, 0x0c010c00u);
-      r[3] = nibpair_to_h2(y, 0x0c030c02u);
-    }
+    r[0] = i8pair_to_h2(x, 0x0c010c00u);
+    r[1] = i8pair_to_h2(x, 0x0c030c02u);
+    r[2] = i8pair_to_h2(y, 0x0c010c00u);
+    r[3] = i8pair_to_h2(y, 0x0c030c02u);
   }
   return __builtin_bit_cast(half8, r);
 }
@@ -474,7 +495,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   float *mk_t = dk_t + 128 * (iMK > 0 ? iMK : 0);
   float *mv_t = dk_t + 128 * (iMV > 0 ? iMV : 0);
   const int n_tiles_all = (j_end - j_begin + kTile - 1) / kTile;
-  const int my_tiles = (a.dbg & 32) ? 0 : (n_tiles_all > w ? (n_tiles_all - w + kWaves - 1) / kWaves : 0);
+  const int my_tiles = (RD4_DEC_KNOBS && (a.dbg & 32)) ? 0 : (n_tiles_all > w ? (n_tiles_all - w + kWaves - 1) / kWaves : 0);
   // Global source of this lane's chunk in load instruction r of a tile:
   // byte offset from the tile's K (or V) base, with the f16 swizzle applied.
   // Rows past the tile's last key (partial tiles) re-read the tile's first row.
@@ -506,7 +527,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     }
   }
   auto issue = [&](int i) {  // i-th tile of this wave
-    if (a.dbg & 2048) return;
+    if (RD4_DEC_KNOBS && (a.dbg & 2048)) return;
     const int j0 = j_begin + (w + i * kWaves) * kTile;
     const int nk = min(kTile, j_end - j0);
     const uint8_t *kt0 = kbase + (int64_t)j0 * kstride;
@@ -537,7 +558,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const int qcw = a.q_f16 ? kHD / 8 : kHD / 4;  // 16-byte chunks per query row
   const int qsb = 16 * (qcw + 1);               // padded row stride in bytes
   auto issue_q = [&]() {  // one load instruction per 64 chunks, spread over the waves
-    if (a.dbg & 2048) return;
+    if (RD4_DEC_KNOBS && (a.dbg & 2048)) return;
     for (int base = 64 * w; base < G * (qcw + 1); base += 64 * kWaves) {
       const int idx = base + lane, r = idx / (qcw + 1), c = idx - r * (qcw + 1);
       if (r < G && c < qcw) {
@@ -585,7 +606,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       float qs = 0.0f;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const float2 f = on ? *(const float2 *)(qrow + k_dim<KT>(b, g, 2 * jj)) : make_float2(0.f, 0.f);
+        const float2 f = on ? make_float2(qrow[k_dim<KT>(b, g, 2 * jj)], qrow[k_dim<KT>(b, g, 2 * jj + 1)])
+                            : make_float2(0.f, 0.f);
         qf[b][2 * jj] = (_Float16)f.x;
         qf[b][2 * jj + 1] = (_Float16)f.y;
         if constexpr (KT == Q4_1) qs += f.x + f.y;
@@ -608,16 +630,14 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       float qs = 0.0f;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int d0 = k_dim<KT>(b, g, 2 * jj);
+        const int d0 = k_dim<KT>(b, g, 2 * jj), d1 = k_dim<KT>(b, g, 2 * jj + 1);
         float x0, x1;
         if (a.q_f16) {
-          const uint32_t u = *(const uint32_t *)(qrow + 2 * d0);
-          x0 = h2f((uint16_t)u);
-          x1 = h2f((uint16_t)(u >> 16));
+          x0 = h2f(*(const uint16_t *)(qrow + 2 * d0));
+          x1 = h2f(*(const uint16_t *)(qrow + 2 * d1));
         } else {
-          const float2 f = *(const float2 *)(qrow + 4 * d0);
-          x0 = f.x;
-          x1 = f.y;
+          x0 = *(const float *)(qrow + 4 * d0);
+          x1 = *(const float *)(qrow + 4 * d1);
         }
         mine[m][jj] = on ? split_prod2(x0, 1.0f, x1, 1.0f, lo_mask) : 0u;
         if constexpr (KT == Q4_1) qs += x0 + x1;
@@ -697,7 +717,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     RD4_TP();
     // ---- S^T = K Q^T: lane holds keys 4g..4g+3 of row n
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (a.dbg & 2) {
+    if (RD4_DEC_KNOBS && (a.dbg & 2)) {
       acc = floatx4{(float)lane, 1.f, 2.f, 3.f};
     } else {
       const uint8_t *krow = kl + n * KS;
@@ -744,9 +764,120 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       sc[i] = v;
       over |= v > m_run + kRescaleLog2;
     }
-    // The reference max moves only when some score passed it by the threshold
-    // (a wave vote); only then is the tile's row max reduced across lanes.
-    if (__any(over)) {
+    // The exp and PV steps are spelled out in both branches of the rescale:
+    // with one copy after the branch, the accumulators reach the PV MFMAs
+    // through a branch merge, and the compiler then gives every MFMA a
+    // result register apart from its C operand and copies all 64 of them
+    // back on every tile. (q5_0 and q4_1 tiles keep one copy: the register
+    // pressure of two spills there.)
+    constexpr bool kSplitPV = KT != Q5_0 && KT != Q4_1 && VT != Q5_0 && VT != Q4_1;
+    auto finish = [&]() __attribute__((always_inline)) {
+      float psum = 0.0f;
+      // a row that has seen no key yet (pair mode, a split holding only the
+      // second token's last key) keeps m_run = -inf; its masked scores give 0
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+  #pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_use);
+        psum += sc[i];
+      }
+      l_run += psum;
+
+      RD4_TP();
+      // ---- O^T += V^T P^T (16 keys)
+      if (RD4_DEC_KNOBS && (a.dbg & 4)) {
+        o[0][0] += sc[0] + sc[3];
+        (void)vl;
+      } else if constexpr (VT == F16) {
+  #if RD4_DEC_PV_HILO
+        const half4 pf = __builtin_bit_cast(
+            half4, u32x2{split_prod2(sc[0], 1.0f, sc[1], 1.0f, lo_mask),
+                         split_prod2(sc[2], 1.0f, sc[3], 1.0f, lo_mask)});
+  #else
+        const half4 pf = hi_only4(sc[0], sc[1], sc[2], sc[3], pmask);
+  #endif
+  #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          // 16-byte chunk n + 16h (dims 8(n + 16h) .. +7) of the lane's 4 keys
+          u32x4 ch[4];
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int row = 4 * g + i;
+            ch[i] = *(const u32x4 *)(vl + row * VS + 16 * ((n ^ (row & 15)) + 16 * h));
+          }
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+            const uint32_t lo = __builtin_amdgcn_perm(ch[1][e >> 1], ch[0][e >> 1], sel);
+            const uint32_t hi = __builtin_amdgcn_perm(ch[3][e >> 1], ch[2][e >> 1], sel);
+            o[8 * h + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{lo, hi}),
+                                                                pf, o[8 * h + e], 0, 0, 0);
+          }
+        }
+      } else {
+        floatx4 dvs[8], mvs[VT == Q4_1 ? 8 : 1];
+        tbl_read8(dv_t + 4 * g, dvs);
+        if constexpr (VT == Q4_1) tbl_read8(mv_t + 4 * g, mvs);
+  #pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const float4 dv = make_float4(dvs[b][0], dvs[b][1], dvs[b][2], dvs[b][3]);
+  #if RD4_DEC_PV_HILO
+          const half4 pf = __builtin_bit_cast(
+              half4, u32x2{split_prod2(sc[0], dv.x, sc[1], dv.y, lo_mask),
+                           split_prod2(sc[2], dv.z, sc[3], dv.w, lo_mask)});
+  #else
+          // P' = f16(p * d) in the hi rows, zero in the lo rows
+          const half4 pf = hi_only4(sc[0] * dv.x, sc[1] * dv.y, sc[2] * dv.z, sc[3] * dv.w, pmask);
+  #endif
+          if constexpr (VT == Q4_1) {
+            if (pair || n < 8) {
+              const float4 mv = make_float4(mvs[b][0], mvs[b][1], mvs[b][2], mvs[b][3]);
+              cm[b] = fmaf(sc[0], mv.x, fmaf(sc[1], mv.y, fmaf(sc[2], mv.z, fmaf(sc[3], mv.w, cm[b]))));
+            }
+          }
+          uint32_t u[4];
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint8_t *blk = vl + (4 * g + i) * VS + block_bytes(VT) * b;
+            const uint8_t *vrow = blk + (VT == Q4_1 ? 4 : VT == Q5_0 ? 6 : 2);
+            u[i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
+            if constexpr (VT == Q5_0) {
+              // element n: low nibble + high bit n; element n + 16: high nibble +
+              // high bit n + 16; as two 5-bit values in bytes 0 and 1
+              const uint32_t hlo = (lds_u16(blk + 2) >> n) & 1u, hhi = (lds_u16(blk + 4) >> n) & 1u;
+              u[i] = (u[i] & 0x0fu) | (hlo << 4) | ((u[i] & 0xf0u) << 4) | (hhi << 12);
+            }
+          }
+          // [key0, key1] and [key2, key3] bytes of the lane's 2-dim (q8_0) or
+          // 2-nibble (q4_0) word, one MFMA per dim
+          const uint32_t w01_0 = __builtin_amdgcn_perm(u[1], u[0], 0x0c040c00u);
+          const uint32_t w23_0 = __builtin_amdgcn_perm(u[3], u[2], 0x0c040c00u);
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  #pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            uint32_t a01, a23;
+            if constexpr (VT == Q5_0) {
+              const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
+              const h2 c = {(_Float16)-1040.0f, (_Float16)-1040.0f};  // 1024 + 16
+              a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) | 0x64006400u) + c);
+              a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) | 0x64006400u) + c);
+            } else if constexpr (VT == Q8_0) {
+              const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
+              const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+              a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) ^ 0x64806480u) + c);
+              a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) ^ 0x64806480u) + c);
+            } else {
+              constexpr int BIAS = VT == Q4_1 ? 0 : -8;
+              a01 = e ? nib_hi_h2<BIAS>(w01_0) : nib_lo_h2<BIAS>(w01_0);
+              a23 = e ? nib_hi_h2<BIAS>(w23_0) : nib_lo_h2<BIAS>(w23_0);
+            }
+            o[2 * b + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{a01, a23}),
+                                                                pf, o[2 * b + e], 0, 0, 0);
+          }
+        }
+      }
+    };
+    auto rescale = [&]() __attribute__((always_inline)) {
       float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       tmax = fmaxf(tmax, xor_f(tmax, 16));
       tmax = fmaxf(tmax, xor_f(tmax, 32));
@@ -761,112 +892,19 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         for (int b = 0; b < 8; ++b) cm[b] *= corr;
       }
       m_run = m_new;
-    }
-    float psum = 0.0f;
-    // a row that has seen no key yet (pair mode, a split holding only the
-    // second token's last key) keeps m_run = -inf; its masked scores give 0
-    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_use);
-      psum += sc[i];
-    }
-    l_run += psum;
-
-    RD4_TP();
-    // ---- O^T += V^T P^T (16 keys)
-    if (a.dbg & 4) {
-      o[0][0] += sc[0] + sc[3];
-      (void)vl;
-    } else if constexpr (VT == F16) {
-#if RD4_DEC_PV_HILO
-      const half4 pf = __builtin_bit_cast(
-          half4, u32x2{split_prod2(sc[0], 1.0f, sc[1], 1.0f, lo_mask),
-                       split_prod2(sc[2], 1.0f, sc[3], 1.0f, lo_mask)});
-#else
-      const half4 pf = hi_only4(sc[0], sc[1], sc[2], sc[3], pmask);
-#endif
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        // 16-byte chunk n + 16h (dims 8(n + 16h) .. +7) of the lane's 4 keys
-        u32x4 ch[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = 4 * g + i;
-          ch[i] = *(const u32x4 *)(vl + row * VS + 16 * ((n ^ (row & 15)) + 16 * h));
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t lo = __builtin_amdgcn_perm(ch[1][e >> 1], ch[0][e >> 1], sel);
-          const uint32_t hi = __builtin_amdgcn_perm(ch[3][e >> 1], ch[2][e >> 1], sel);
-          o[8 * h + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{lo, hi}),
-                                                              pf, o[8 * h + e], 0, 0, 0);
-        }
+    };
+    // The reference max moves only when some score passed it by the threshold
+    // (a wave vote); only then is the tile's row max reduced across lanes.
+    if constexpr (kSplitPV) {
+      if (__any(over)) {
+        rescale();
+        finish();
+      } else {
+        finish();
       }
     } else {
-      floatx4 dvs[8], mvs[VT == Q4_1 ? 8 : 1];
-      tbl_read8(dv_t + 4 * g, dvs);
-      if constexpr (VT == Q4_1) tbl_read8(mv_t + 4 * g, mvs);
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const float4 dv = make_float4(dvs[b][0], dvs[b][1], dvs[b][2], dvs[b][3]);
-#if RD4_DEC_PV_HILO
-        const half4 pf = __builtin_bit_cast(
-            half4, u32x2{split_prod2(sc[0], dv.x, sc[1], dv.y, lo_mask),
-                         split_prod2(sc[2], dv.z, sc[3], dv.w, lo_mask)});
-#else
-        // P' = f16(p * d) in the hi rows, zero in the lo rows
-        const half4 pf = hi_only4(sc[0] * dv.x, sc[1] * dv.y, sc[2] * dv.z, sc[3] * dv.w, pmask);
-#endif
-        if constexpr (VT == Q4_1) {
-          if (pair || n < 8) {
-            const float4 mv = make_float4(mvs[b][0], mvs[b][1], mvs[b][2], mvs[b][3]);
-            cm[b] = fmaf(sc[0], mv.x, fmaf(sc[1], mv.y, fmaf(sc[2], mv.z, fmaf(sc[3], mv.w, cm[b]))));
-          }
-        }
-        uint32_t u[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint8_t *blk = vl + (4 * g + i) * VS + block_bytes(VT) * b;
-          const uint8_t *vrow = blk + (VT == Q4_1 ? 4 : VT == Q5_0 ? 6 : 2);
-          u[i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
-          if constexpr (VT == Q5_0) {
-            // element n: low nibble + high bit n; element n + 16: high nibble +
-            // high bit n + 16; as two 5-bit values in bytes 0 and 1
-            const uint32_t hlo = (lds_u16(blk + 2) >> n) & 1u, hhi = (lds_u16(blk + 4) >> n) & 1u;
-            u[i] = (u[i] & 0x0fu) | (hlo << 4) | ((u[i] & 0xf0u) << 4) | (hhi << 12);
-          }
-        }
-        // [key0, key1] and [key2, key3] bytes of the lane's 2-dim (q8_0) or
-        // 2-nibble (q4_0) word, one MFMA per dim
-        const uint32_t w01_0 = __builtin_amdgcn_perm(u[1], u[0], 0x0c040c00u);
-        const uint32_t w23_0 = __builtin_amdgcn_perm(u[3], u[2], 0x0c040c00u);
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          uint32_t a01, a23;
-          if constexpr (VT == Q5_0) {
-            const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
-            const h2 c = {(_Float16)-1040.0f, (_Float16)-1040.0f};  // 1024 + 16
-            a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) | 0x64006400u) + c);
-            a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) | 0x64006400u) + c);
-          } else if constexpr (VT == Q8_0) {
-            const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
-            const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-            a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) ^ 0x64806480u) + c);
-            a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) ^ 0x64806480u) + c);
-          } else {
-            constexpr float kBias = VT == Q4_1 ? -1024.0f : -1032.0f;  // 1024 + (0 or 8)
-            const h2 c = {(_Float16)kBias, (_Float16)kBias};
-            const int sh = 4 * e;
-            a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ((w01_0 >> sh) & 0x000f000fu) | 0x64006400u) + c);
-            a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ((w23_0 >> sh) & 0x000f000fu) | 0x64006400u) + c);
-          }
-          o[2 * b + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{a01, a23}),
-                                                              pf, o[2 * b + e], 0, 0, 0);
-        }
-      }
+      if (__any(over)) rescale();
+      finish();
     }
   }
 
