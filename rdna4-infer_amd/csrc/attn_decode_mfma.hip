@@ -51,6 +51,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // profiling knobs (RD4_DECODE_DBG bits 2, 4, 32, 2048 skip the QK product, the PV
 // product, all tiles, all loads); off in production builds, where their
 // branches cost register copies in the tile loop
+#ifndef RD4_DEC_QLDS
+#define RD4_DEC_QLDS 1
+#endif
 #ifndef RD4_DEC_KNOBS
 #define RD4_DEC_KNOBS 0
 #endif
@@ -659,15 +662,26 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     __syncthreads();
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
+#if !RD4_DEC_QLDS
       qf[b] = __builtin_bit_cast(half8, qf_lds[b * 64 + lane]);
+#endif
       // the offset term goes to the hi rows only (rows n and n^8 are summed)
       if constexpr (KT == Q4_1) qblk[b] = n < 8 ? qsum_lds[b * 8 + n] : 0.0f;
     }
   }
+  // Query fragment of block b for the QK product: pair mode keeps its eight in
+  // registers; single-token mode reads them from LDS at each use, which frees
+  // 32 VGPRs in the tile loop
+  auto q_frag = [&](int b) __attribute__((always_inline)) {
+#if RD4_DEC_QLDS
+    if constexpr (!PAIR) return __builtin_bit_cast(half8, ((const u32x4 *)q_lds)[b * 64 + lane]);
+#endif
+    return qf[b];
+  };
   const float sl2 = a.scale * kLog2e;
-  // edge gather of the unaligned quantized-K blocks: lane group 3 (q8_0) or
-  // the odd lane groups (q4_0) take the block's first and last byte pairs
-  const uint32_t sel_edge = (KT == Q8_0 ? g == 3 : (g & 1) == 1) ? 0x05040302u : 0x07060504u;
+  // edge gather of the unaligned q8_0 K blocks: lane group 3 takes the block's
+  // first and last byte pairs
+  const uint32_t sel_edge = g == 3 ? 0x05040302u : 0x07060504u;
   // pair mode: the last key of this lane's row; the P operand fills all 16 rows
   const int row_last = pair ? a.t + tok + (n >> 3) : t;
   const uint32_t pmask = pair ? 0u : lo_mask;
@@ -680,232 +694,237 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   for (int b = 0; b < 8; ++b) cm[b] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
-  RD4_TP();
-  for (int i = 0; i < my_tiles; ++i) {
-    RD4_TP();
-    const int nk = min(kTile, j_end - (j_begin + (w + i * kWaves) * kTile));
-    if (i + R - 1 < my_tiles) {
-      // the stage being refilled was read by the previous iteration: those reads are done
-      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue(i + R - 1);
-    }
-    // tile i is complete once at most the loads of the tiles issued after it remain
-    const int after = min(R - 1, my_tiles - 1 - i);
-    if (after >= 3) wait_vm<3 * NI>();
-    else if (after == 2) wait_vm<2 * NI>();
-    else if (after == 1) wait_vm<NI>();
-    else wait_vm<0>();
-    wave_sync();
-    RD4_TP();
-    const uint8_t *kl = ring + (i % R) * TB;
-    const uint8_t *vl = kl + KCH * 16;
-    if constexpr (DT > 0) {  // f16 scales (and offsets) of the tile -> f32 tables, once per tile
-#pragma unroll
-      for (int j = 0; j < DT / 256; ++j) {
-        const int v = lane + 64 * j;
-        const int ti = v >> 7, key = v & 15, b = (v >> 4) & 7;
-        float d;
-        if (ti == iDK) d = scale_of<KT>(kl + key * KS, b);
-        else if (ti == iDV) d = scale_of<VT>(vl + key * VS, b);
-        else if (ti == iMK) d = offset_of<KT>(kl + key * KS, b);
-        else d = offset_of<VT>(vl + key * VS, b);
-        dk_t[v] = d;
-      }
-      wave_sync();
-    }
-
-    RD4_TP();
-    // ---- S^T = K Q^T: lane holds keys 4g..4g+3 of row n
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (RD4_DEC_KNOBS && (a.dbg & 2)) {
-      acc = floatx4{(float)lane, 1.f, 2.f, 3.f};
-    } else {
-      const uint8_t *krow = kl + n * KS;
-      if constexpr (KT == F16) {
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), qf[b], acc, 0, 0, 0);
-      } else {
-        floatx4 dks[8], mks[KT == Q4_1 ? 8 : 1];
-        tbl_read8(dk_t + 4 * g, dks);
-        if constexpr (KT == Q4_1) tbl_read8(mk_t + 4 * g, mks);
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-          const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-          const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), qf[b], z, 0, 0, 0);
-          const float4 dk = make_float4(dks[b][0], dks[b][1], dks[b][2], dks[b][3]);
-          acc[0] = fmaf(dk.x, c[0], acc[0]);
-          acc[1] = fmaf(dk.y, c[1], acc[1]);
-          acc[2] = fmaf(dk.z, c[2], acc[2]);
-          acc[3] = fmaf(dk.w, c[3], acc[3]);
-          if constexpr (KT == Q4_1) {
-            const float4 mk = make_float4(mks[b][0], mks[b][1], mks[b][2], mks[b][3]);
-            acc[0] = fmaf(mk.x, qblk[b], acc[0]);
-            acc[1] = fmaf(mk.y, qblk[b], acc[1]);
-            acc[2] = fmaf(mk.z, qblk[b], acc[2]);
-            acc[3] = fmaf(mk.w, qblk[b], acc[3]);
-          }
-        }
-      }
-    }
-    RD4_TP();
-    // Rows n and n^8 are the hi and lo halves of the same head. (A DPP
-    // row_ror:8 add was tried here; the compiler's DPP combine fed acc[0] to
-    // all four adds, so the exchange stays a plain lane shuffle.)
-    float sc[4];
-    bool over = false;
-    // last key this lane's row may see, relative to the tile: pair mode masks the
-    // second token's last key in the first token's rows
-    const int lim = pair ? min(nk - 1, row_last - (j_begin + (w + i * kWaves) * kTile)) : nk - 1;
+  // state of the current tile, shared by the exp/PV step and the rescale
+  float sc[4];
+  const uint8_t *vl = nullptr;
+  auto finish = [&]() __attribute__((always_inline)) {
+    float psum = 0.0f;
+    // a row that has seen no key yet (pair mode, a split holding only the
+    // second token's last key) keeps m_run = -inf; its masked scores give 0
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v = pair ? acc[i] * sl2 : (acc[i] + xor_f(acc[i], 8)) * sl2;
-      if (4 * g + i > lim) v = -INFINITY;
-      sc[i] = v;
-      over |= v > m_run + kRescaleLog2;
+      sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_use);
+      psum += sc[i];
     }
-    // The exp and PV steps are spelled out in both branches of the rescale:
-    // with one copy after the branch, the accumulators reach the PV MFMAs
-    // through a branch merge, and the compiler then gives every MFMA a
-    // result register apart from its C operand and copies all 64 of them
-    // back on every tile. (q5_0 and q4_1 tiles keep one copy: the register
-    // pressure of two spills there.)
-    constexpr bool kSplitPV = KT != Q5_0 && KT != Q4_1 && VT != Q5_0 && VT != Q4_1;
-    auto finish = [&]() __attribute__((always_inline)) {
-      float psum = 0.0f;
-      // a row that has seen no key yet (pair mode, a split holding only the
-      // second token's last key) keeps m_run = -inf; its masked scores give 0
-      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-  #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_use);
-        psum += sc[i];
-      }
-      l_run += psum;
+    l_run += psum;
 
-      RD4_TP();
-      // ---- O^T += V^T P^T (16 keys)
-      if (RD4_DEC_KNOBS && (a.dbg & 4)) {
-        o[0][0] += sc[0] + sc[3];
-        (void)vl;
-      } else if constexpr (VT == F16) {
-  #if RD4_DEC_PV_HILO
-        const half4 pf = __builtin_bit_cast(
-            half4, u32x2{split_prod2(sc[0], 1.0f, sc[1], 1.0f, lo_mask),
-                         split_prod2(sc[2], 1.0f, sc[3], 1.0f, lo_mask)});
-  #else
-        const half4 pf = hi_only4(sc[0], sc[1], sc[2], sc[3], pmask);
-  #endif
-  #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          // 16-byte chunk n + 16h (dims 8(n + 16h) .. +7) of the lane's 4 keys
-          u32x4 ch[4];
-  #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int row = 4 * g + i;
-            ch[i] = *(const u32x4 *)(vl + row * VS + 16 * ((n ^ (row & 15)) + 16 * h));
-          }
-  #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            const uint32_t lo = __builtin_amdgcn_perm(ch[1][e >> 1], ch[0][e >> 1], sel);
-            const uint32_t hi = __builtin_amdgcn_perm(ch[3][e >> 1], ch[2][e >> 1], sel);
-            o[8 * h + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{lo, hi}),
-                                                                pf, o[8 * h + e], 0, 0, 0);
-          }
-        }
-      } else {
-        floatx4 dvs[8], mvs[VT == Q4_1 ? 8 : 1];
-        tbl_read8(dv_t + 4 * g, dvs);
-        if constexpr (VT == Q4_1) tbl_read8(mv_t + 4 * g, mvs);
-  #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-          const float4 dv = make_float4(dvs[b][0], dvs[b][1], dvs[b][2], dvs[b][3]);
-  #if RD4_DEC_PV_HILO
-          const half4 pf = __builtin_bit_cast(
-              half4, u32x2{split_prod2(sc[0], dv.x, sc[1], dv.y, lo_mask),
-                           split_prod2(sc[2], dv.z, sc[3], dv.w, lo_mask)});
-  #else
-          // P' = f16(p * d) in the hi rows, zero in the lo rows
-          const half4 pf = hi_only4(sc[0] * dv.x, sc[1] * dv.y, sc[2] * dv.z, sc[3] * dv.w, pmask);
-  #endif
-          if constexpr (VT == Q4_1) {
-            if (pair || n < 8) {
-              const float4 mv = make_float4(mvs[b][0], mvs[b][1], mvs[b][2], mvs[b][3]);
-              cm[b] = fmaf(sc[0], mv.x, fmaf(sc[1], mv.y, fmaf(sc[2], mv.z, fmaf(sc[3], mv.w, cm[b]))));
-            }
-          }
-          uint32_t u[4];
-  #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint8_t *blk = vl + (4 * g + i) * VS + block_bytes(VT) * b;
-            const uint8_t *vrow = blk + (VT == Q4_1 ? 4 : VT == Q5_0 ? 6 : 2);
-            u[i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
-            if constexpr (VT == Q5_0) {
-              // element n: low nibble + high bit n; element n + 16: high nibble +
-              // high bit n + 16; as two 5-bit values in bytes 0 and 1
-              const uint32_t hlo = (lds_u16(blk + 2) >> n) & 1u, hhi = (lds_u16(blk + 4) >> n) & 1u;
-              u[i] = (u[i] & 0x0fu) | (hlo << 4) | ((u[i] & 0xf0u) << 4) | (hhi << 12);
-            }
-          }
-          // [key0, key1] and [key2, key3] bytes of the lane's 2-dim (q8_0) or
-          // 2-nibble (q4_0) word, one MFMA per dim
-          const uint32_t w01_0 = __builtin_amdgcn_perm(u[1], u[0], 0x0c040c00u);
-          const uint32_t w23_0 = __builtin_amdgcn_perm(u[3], u[2], 0x0c040c00u);
-          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            uint32_t a01, a23;
-            if constexpr (VT == Q5_0) {
-              const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
-              const h2 c = {(_Float16)-1040.0f, (_Float16)-1040.0f};  // 1024 + 16
-              a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) | 0x64006400u) + c);
-              a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) | 0x64006400u) + c);
-            } else if constexpr (VT == Q8_0) {
-              const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
-              const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-              a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) ^ 0x64806480u) + c);
-              a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) ^ 0x64806480u) + c);
-            } else {
-              constexpr int BIAS = VT == Q4_1 ? 0 : -8;
-              a01 = e ? nib_hi_h2<BIAS>(w01_0) : nib_lo_h2<BIAS>(w01_0);
-              a23 = e ? nib_hi_h2<BIAS>(w23_0) : nib_lo_h2<BIAS>(w23_0);
-            }
-            o[2 * b + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{a01, a23}),
-                                                                pf, o[2 * b + e], 0, 0, 0);
-          }
-        }
-      }
-    };
-    auto rescale = [&]() __attribute__((always_inline)) {
-      float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      tmax = fmaxf(tmax, xor_f(tmax, 16));
-      tmax = fmaxf(tmax, xor_f(tmax, 32));
-      const float m_new = fmaxf(m_run, tmax);
-      // a row whose max did not move (also -inf, a row with no key yet) keeps its state
-      const float corr = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= corr;
+    RD4_TP();
+    // ---- O^T += V^T P^T (16 keys)
+    if (RD4_DEC_KNOBS && (a.dbg & 4)) {
+      o[0][0] += sc[0] + sc[3];
+      (void)vl;
+    } else if constexpr (VT == F16) {
+#if RD4_DEC_PV_HILO
+      const half4 pf = __builtin_bit_cast(
+          half4, u32x2{split_prod2(sc[0], 1.0f, sc[1], 1.0f, lo_mask),
+                       split_prod2(sc[2], 1.0f, sc[3], 1.0f, lo_mask)});
+#else
+      const half4 pf = hi_only4(sc[0], sc[1], sc[2], sc[3], pmask);
+#endif
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[i] *= corr;
-      if constexpr (VT == Q4_1) {
+      for (int h = 0; h < 2; ++h) {
+        // 16-byte chunk n + 16h (dims 8(n + 16h) .. +7) of the lane's 4 keys
+        u32x4 ch[4];
 #pragma unroll
-        for (int b = 0; b < 8; ++b) cm[b] *= corr;
-      }
-      m_run = m_new;
-    };
-    // The reference max moves only when some score passed it by the threshold
-    // (a wave vote); only then is the tile's row max reduced across lanes.
-    if constexpr (kSplitPV) {
-      if (__any(over)) {
-        rescale();
-        finish();
-      } else {
-        finish();
+        for (int i = 0; i < 4; ++i) {
+          const int row = 4 * g + i;
+          ch[i] = *(const u32x4 *)(vl + row * VS + 16 * ((n ^ (row & 15)) + 16 * h));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          const uint32_t lo = __builtin_amdgcn_perm(ch[1][e >> 1], ch[0][e >> 1], sel);
+          const uint32_t hi = __builtin_amdgcn_perm(ch[3][e >> 1], ch[2][e >> 1], sel);
+          o[8 * h + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{lo, hi}),
+                                                              pf, o[8 * h + e], 0, 0, 0);
+        }
       }
     } else {
-      if (__any(over)) rescale();
+      floatx4 dvs[8], mvs[VT == Q4_1 ? 8 : 1];
+      tbl_read8(dv_t + 4 * g, dvs);
+      if constexpr (VT == Q4_1) tbl_read8(mv_t + 4 * g, mvs);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const float4 dv = make_float4(dvs[b][0], dvs[b][1], dvs[b][2], dvs[b][3]);
+#if RD4_DEC_PV_HILO
+        const half4 pf = __builtin_bit_cast(
+            half4, u32x2{split_prod2(sc[0], dv.x, sc[1], dv.y, lo_mask),
+                         split_prod2(sc[2], dv.z, sc[3], dv.w, lo_mask)});
+#else
+        // P' = f16(p * d) in the hi rows, zero in the lo rows
+        const half4 pf = hi_only4(sc[0] * dv.x, sc[1] * dv.y, sc[2] * dv.z, sc[3] * dv.w, pmask);
+#endif
+        if constexpr (VT == Q4_1) {
+          if (pair || n < 8) {
+            const float4 mv = make_float4(mvs[b][0], mvs[b][1], mvs[b][2], mvs[b][3]);
+            cm[b] = fmaf(sc[0], mv.x, fmaf(sc[1], mv.y, fmaf(sc[2], mv.z, fmaf(sc[3], mv.w, cm[b]))));
+          }
+        }
+        uint32_t u[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint8_t *blk = vl + (4 * g + i) * VS + block_bytes(VT) * b;
+          const uint8_t *vrow = blk + (VT == Q4_1 ? 4 : VT == Q5_0 ? 6 : 2);
+          u[i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
+          if constexpr (VT == Q5_0) {
+            // element n: low nibble + high bit n; element n + 16: high nibble +
+            // high bit n + 16; as two 5-bit values in bytes 0 and 1
+            const uint32_t hlo = (lds_u16(blk + 2) >> n) & 1u, hhi = (lds_u16(blk + 4) >> n) & 1u;
+            u[i] = (u[i] & 0x0fu) | (hlo << 4) | ((u[i] & 0xf0u) << 4) | (hhi << 12);
+          }
+        }
+        // [key0, key1] and [key2, key3] bytes of the lane's 2-dim (q8_0) or
+        // 2-nibble (q4_0) word, one MFMA per dim
+        const uint32_t w01_0 = __builtin_amdgcn_perm(u[1], u[0], 0x0c040c00u);
+        const uint32_t w23_0 = __builtin_amdgcn_perm(u[3], u[2], 0x0c040c00u);
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          uint32_t a01, a23;
+          if constexpr (VT == Q5_0) {
+            const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
+            const h2 c = {(_Float16)-1040.0f, (_Float16)-1040.0f};  // 1024 + 16
+            a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) | 0x64006400u) + c);
+            a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) | 0x64006400u) + c);
+          } else if constexpr (VT == Q8_0) {
+            const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
+            const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+            a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) ^ 0x64806480u) + c);
+            a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) ^ 0x64806480u) + c);
+          } else {
+            constexpr int BIAS = VT == Q4_1 ? 0 : -8;
+            a01 = e ? nib_hi_h2<BIAS>(w01_0) : nib_lo_h2<BIAS>(w01_0);
+            a23 = e ? nib_hi_h2<BIAS>(w23_0) : nib_lo_h2<BIAS>(w23_0);
+          }
+          o[2 * b + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, u32x2{a01, a23}),
+                                                              pf, o[2 * b + e], 0, 0, 0);
+        }
+      }
+    }
+  };
+  auto rescale = [&]() __attribute__((always_inline)) {
+    float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    tmax = fmaxf(tmax, xor_f(tmax, 16));
+    tmax = fmaxf(tmax, xor_f(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    // a row whose max did not move (also -inf, a row with no key yet) keeps its state
+    const float corr = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    l_run *= corr;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] *= corr;
+    if constexpr (VT == Q4_1) {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) cm[b] *= corr;
+    }
+    m_run = m_new;
+  };
+
+  // The tile loop proper never rescales: a tile whose scores pass the running
+  // max by the threshold leaves it, is rescaled and finished here, and the loop
+  // resumes with the next tile. (With the rescale as a branch inside the loop,
+  // the accumulators reach the PV MFMAs through a branch merge, and the
+  // compiler gives every MFMA a result register apart from its C operand and
+  // copies all 64 back on every tile.)
+  RD4_TP();
+  int i = 0;
+  for (;;) {
+    bool rescale_due = false;
+    for (; i < my_tiles; ++i) {
+      RD4_TP();
+      const int nk = min(kTile, j_end - (j_begin + (w + i * kWaves) * kTile));
+      if (i + R - 1 < my_tiles) {
+        // the stage being refilled was read by the previous iteration: those reads are done
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(i + R - 1);
+      }
+      // tile i is complete once at most the loads of the tiles issued after it remain
+      const int after = min(R - 1, my_tiles - 1 - i);
+      if (after >= 3) wait_vm<3 * NI>();
+      else if (after == 2) wait_vm<2 * NI>();
+      else if (after == 1) wait_vm<NI>();
+      else wait_vm<0>();
+      wave_sync();
+      RD4_TP();
+      const uint8_t *kl = ring + (i % R) * TB;
+      vl = kl + KCH * 16;
+      if constexpr (DT > 0) {  // f16 scales (and offsets) of the tile -> f32 tables, once per tile
+#pragma unroll
+        for (int j = 0; j < DT / 256; ++j) {
+          const int v = lane + 64 * j;
+          const int ti = v >> 7, key = v & 15, b = (v >> 4) & 7;
+          float d;
+          if (ti == iDK) d = scale_of<KT>(kl + key * KS, b);
+          else if (ti == iDV) d = scale_of<VT>(vl + key * VS, b);
+          else if (ti == iMK) d = offset_of<KT>(kl + key * KS, b);
+          else d = offset_of<VT>(vl + key * VS, b);
+          dk_t[v] = d;
+        }
+        wave_sync();
+      }
+
+      RD4_TP();
+      // ---- S^T = K Q^T: lane holds keys 4g..4g+3 of row n
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (RD4_DEC_KNOBS && (a.dbg & 2)) {
+        acc = floatx4{(float)lane, 1.f, 2.f, 3.f};
+      } else {
+        const uint8_t *krow = kl + n * KS;
+        if constexpr (KT == F16) {
+#pragma unroll
+          for (int b = 0; b < 8; ++b)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), q_frag(b), acc, 0, 0, 0);
+        } else {
+          floatx4 dks[8], mks[KT == Q4_1 ? 8 : 1];
+          tbl_read8(dk_t + 4 * g, dks);
+          if constexpr (KT == Q4_1) tbl_read8(mk_t + 4 * g, mks);
+#pragma unroll
+          for (int b = 0; b < 8; ++b) {
+            const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+            const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), q_frag(b), z, 0, 0, 0);
+            const float4 dk = make_float4(dks[b][0], dks[b][1], dks[b][2], dks[b][3]);
+            acc[0] = fmaf(dk.x, c[0], acc[0]);
+            acc[1] = fmaf(dk.y, c[1], acc[1]);
+            acc[2] = fmaf(dk.z, c[2], acc[2]);
+            acc[3] = fmaf(dk.w, c[3], acc[3]);
+            if constexpr (KT == Q4_1) {
+              const float4 mk = make_float4(mks[b][0], mks[b][1], mks[b][2], mks[b][3]);
+              acc[0] = fmaf(mk.x, qblk[b], acc[0]);
+              acc[1] = fmaf(mk.y, qblk[b], acc[1]);
+              acc[2] = fmaf(mk.z, qblk[b], acc[2]);
+              acc[3] = fmaf(mk.w, qblk[b], acc[3]);
+            }
+          }
+        }
+      }
+      RD4_TP();
+      // Rows n and n^8 are the hi and lo halves of the same head. (A DPP
+      // row_ror:8 add was tried here; the compiler's DPP combine fed acc[0] to
+      // all four adds, so the exchange stays a plain lane shuffle.)
+      bool over = false;
+      // last key this lane's row may see, relative to the tile: pair mode masks the
+      // second token's last key in the first token's rows
+      const int lim = pair ? min(nk - 1, row_last - (j_begin + (w + i * kWaves) * kTile)) : nk - 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = pair ? acc[i] * sl2 : (acc[i] + xor_f(acc[i], 8)) * sl2;
+        if (4 * g + i > lim) v = -INFINITY;
+        sc[i] = v;
+        over |= v > m_run + kRescaleLog2;
+      }
+      // The running max moves only when some score passed it by the threshold
+      // (a wave vote); only then is the tile's row max reduced across lanes, in
+      // the rare path after this loop.
+      if (__any(over)) {
+        rescale_due = true;
+        break;
+      }
       finish();
     }
+    if (!rescale_due) break;
+    rescale();
+    finish();
+    ++i;
   }
 
   RD4_TP();
