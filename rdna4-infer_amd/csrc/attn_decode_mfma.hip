@@ -175,6 +175,15 @@ __host__ __device__ constexpr int k_dim(int b, int g, int j) {
   return 32 * b + (j < 4 ? 26 + j : j == 4 ? 0 : j == 5 ? 1 : j == 6 ? 30 : 31);
 }
 
+// k-slot (g, j) of dim e (0..31) of block b under k_dim<Q8_0>: the inverse map,
+// used to lay the int8 query rows out in fragment order.
+__device__ __forceinline__ int q8_slot(int b, int e) {
+  if (b & 1) return e;  // g = e / 8, j = e % 8
+  if (e >= 2 && e < 26) return e - 2;
+  return e < 2 ? 28 + e : (e < 30 ? 24 + (e - 26) : 30 + (e - 30));
+}
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
 // (x & m) | b in one VALU instruction (the compiler splits it into two
 // literal-operand ops; VOP3 on this target takes no literal, so m comes from
 // an SGPR)
@@ -305,6 +314,52 @@ __device__ __forceinline__ half8 k_frag(const uint8_t *krow, int b, int g, int n
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// The words of one q8_0 key row that lane group g needs for the int8 product
+// S^T = K Q^T, read in one asm batch that waits for its own LDS reads (through
+// ordinary loads the compiler cannot tell them from the tile DMA still in
+// flight and waits for that first). kw[2b], kw[2b + 1]: the two words of block
+// b at k-slots 0-3 and 4-7 (even blocks: the aligned words at +4 and +8 + 8g);
+// ke[b / 2]: the first word of even block b (its d and first two quants).
+__device__ __forceinline__ void k_words_q8(const uint8_t *krow, int g, uint32_t (&kw)[16], uint32_t (&ke)[4]) {
+  const uint32_t kb = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)(krow + 8 * g);
+  const uint32_t kr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)krow;
+  // dword offsets: even b = 2m: 17m + 1, 17m + 2; odd b = 2m + 1: 17m + 9, 17m + 10
+  u32x2 r[10];
+  __asm__ volatile(
+      "ds_read2_b32 %0, %10 offset0:1 offset1:2\n\t"
+      "ds_read2_b32 %1, %10 offset0:9 offset1:10\n\t"
+      "ds_read2_b32 %2, %10 offset0:18 offset1:19\n\t"
+      "ds_read2_b32 %3, %10 offset0:26 offset1:27\n\t"
+      "ds_read2_b32 %4, %10 offset0:35 offset1:36\n\t"
+      "ds_read2_b32 %5, %10 offset0:43 offset1:44\n\t"
+      "ds_read2_b32 %6, %10 offset0:52 offset1:53\n\t"
+      "ds_read2_b32 %7, %10 offset0:60 offset1:61\n\t"
+      "ds_read2_b32 %8, %11 offset0:0 offset1:17\n\t"
+      "ds_read2_b32 %9, %11 offset0:34 offset1:51\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
+        "=&v"(r[7]), "=&v"(r[8]), "=&v"(r[9])
+      : "v"(kb), "v"(kr)
+      : "memory");
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    kw[2 * i] = r[i][0];
+    kw[2 * i + 1] = r[i][1];
+  }
+  ke[0] = r[8][0];
+  ke[1] = r[8][1];
+  ke[2] = r[9][0];
+  ke[3] = r[9][1];
+}
+// A operand of the int8 product for block b: the same 8 bytes (k-slots 0..7 of
+// k_dim<Q8_0>) that k_frag converts, left as int8.
+__device__ __forceinline__ long k_op_i8(const uint32_t (&kw)[16], const uint32_t (&ke)[4], int b,
+                                        uint32_t sel_edge) {
+  const uint32_t x = kw[2 * b];
+  const uint32_t y = (b & 1) ? kw[2 * b + 1] : __builtin_amdgcn_perm(kw[2 * b + 1], ke[b >> 1], sel_edge);
+  return (long)(((uint64_t)y << 32) | x);
+}
+
 // Dim of head_dim that row r' (0..15) of PV MFMA t (0..15) accumulates. The V
 // operand lane with MFMA row r reads whole aligned words of its 4 keys:
 //   f16:  16-byte chunk r + 16h (dims 8(r + 16h) .. +7), one MFMA per dim, t = 8h + e;
@@ -366,9 +421,6 @@ __device__ __forceinline__ uint32_t split_prod2(float p0, float d0, float p1, fl
           : "v"(p0), "v"(d0), "v"(m), "v"(p1), "v"(d1));
   return r;
 }
-#ifndef RD4_DEC_PV_HILO
-#define RD4_DEC_PV_HILO 0
-#endif
 // The 8 per-block float4 entries p[16 b .. 16 b + 3] of a per-tile scale table,
 // read with one asm block that waits for its own LDS reads. Through ordinary
 // loads the compiler places a vmcnt(0) before them (it cannot rule out that the
@@ -391,13 +443,13 @@ __device__ __forceinline__ void tbl_read8(const float *p, floatx4 (&out)[8]) {
       : "v"(a)
       : "memory");
 }
-// f16 of four products in the rows n < 8 (lo_mask = 0 there) and zero in the
-// rows n >= 8, as the B operand of one PV MFMA.
-__device__ __forceinline__ half4 hi_only4(float x0, float x1, float x2, float x3, uint32_t lo_mask) {
+// f16 of four products, the B operand of one PV MFMA. In single-token mode
+// rows n and n + 8 carry the same head (the hi and lo query parts were summed
+// into both), so their O columns come out identical and rows 8-15 are ignored.
+__device__ __forceinline__ half4 p_op4(float x0, float x1, float x2, float x3) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const h2 a = {(_Float16)x0, (_Float16)x1}, b = {(_Float16)x2, (_Float16)x3};
-  return __builtin_bit_cast(half4, u32x2{__builtin_bit_cast(uint32_t, a) & ~lo_mask,
-                                         __builtin_bit_cast(uint32_t, b) & ~lo_mask});
+  return __builtin_bit_cast(half4, u32x2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)});
 }
 // Online-softmax reference max: moved only when a row's new scores exceed it
 // by more than kRescaleLog2 (probabilities stay <= 2^8 against a stale max),
@@ -408,6 +460,16 @@ __device__ __forceinline__ half4 hi_only4(float x0, float x1, float x2, float x3
 constexpr float kRescaleLog2 = RD4_DEC_THRESH;
 
 }  // namespace
+#if RD4_DEC_TRACE
+__device__ unsigned long long rd4_dec_trace[1024 * 8 * 32];
+extern "C" int rd4_dec_trace_read(void *host) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(rd4_dec_trace), sizeof(rd4_dec_trace));
+}
+extern "C" int rd4_dec_trace_clear() {
+  static unsigned long long z[1024 * 8 * 32];
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(rd4_dec_trace), z, sizeof(z));
+}
+#endif
 
 template <int KT, int VT, bool PAIR>
 __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfma_kernel(AttnArgs a) {
@@ -418,6 +480,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   constexpr int KC = TS::KC, VC = TS::VC, KCH = TS::KCH, VCH = TS::VCH, NI = TS::NI;
   constexpr int TB = TS::TB, R = TS::R, DT = TS::DT;
 
+  // q8_0 K in single-token mode: S^T on the int8 MFMA, the query as int8 hi and
+  // lo rows (q = s_hi q_hi + s_lo q_lo to ~amax / 65000 per row)
+  constexpr bool kI8 = KT == Q8_0 && !PAIR;
   const int s = blockIdx.x;
   const int kvh = blockIdx.y / a.n_chunks;
   const int hc = blockIdx.y - kvh * a.n_chunks;
@@ -431,12 +496,14 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
 #if RD4_DEC_TRACE
-  // timestamps of CTA (0,0): slot [w][point] in a.out as u64 (diagnostic builds only)
+  // timestamps (100 MHz realtime counter) of lane 0 of every wave, slot
+  // [cta][wave][point] of rd4_dec_trace (diagnostic builds only)
   int tpos = 0;
-#define RD4_TP()                                                                        \
-  do {                                                                                  \
-    if (blockIdx.x == 0 && blockIdx.y == 0 && lane == 0 && tpos < 60)                   \
-      ((unsigned long long *)a.out)[w * 64 + tpos++] = __builtin_amdgcn_s_memtime();    \
+  const int tcta = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+#define RD4_TP()                                                                          \
+  do {                                                                                    \
+    if (lane == 0 && tpos < 32 && tcta < 1024)                                            \
+      rd4_dec_trace[(tcta * 8 + w) * 32 + tpos++] = __builtin_amdgcn_s_memrealtime();     \
   } while (0)
 #else
 #define RD4_TP() \
@@ -599,6 +666,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const uint32_t lo_mask = n >= 8 ? 0xffffffffu : 0u;
   half8 qf[8];
   float qblk[8];
+  long qop[kI8 ? 8 : 1];  // int8 query fragments (kI8)
+  float sqr = 0.0f;       // this lane's row scale (kI8)
   if (pair) {
     // f16 query rows straight from global memory, both tokens' heads
     const int hh = n & 7, tr = n >> 3;
@@ -621,6 +690,49 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         qblk[b] = qs;
       }
     }
+  } else if constexpr (kI8) {
+    // wave w quantizes head rows w, w + kWaves, ...: lane l holds dims 4l..4l+3;
+    // s_hi = amax / 127, q_hi = rint(q / s_hi), and the remainder on s_hi / 254
+    float xr[8 / kWaves][4];
+#pragma unroll
+    for (int m = 0; m < 8 / kWaves; ++m) {
+      const int r = w + kWaves * m;
+      const uint8_t *qrow = q_lds + (r < G ? r : 0) * qsb;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xr[m][i] = r >= G ? 0.0f
+                   : a.q_f16 ? h2f(*(const uint16_t *)(qrow + 2 * (4 * lane + i)))
+                             : *(const float *)(qrow + 4 * (4 * lane + i));
+    }
+    __syncthreads();  // every wave has read the query rows
+    uint8_t *qi = q_lds;                          // [16 rows][8 blocks][4 g][8 bytes]
+    float *sq = (float *)(q_lds + 16 * kHD);      // [16] row scales (with scale * log2 e)
+#pragma unroll
+    for (int m = 0; m < 8 / kWaves; ++m) {
+      const int r = w + kWaves * m;
+      float am = fmaxf(fmaxf(fabsf(xr[m][0]), fabsf(xr[m][1])), fmaxf(fabsf(xr[m][2]), fabsf(xr[m][3])));
+#pragma unroll
+      for (int x = 1; x < 64; x <<= 1) am = fmaxf(am, xor_f(am, x));
+      const float s_hi = am / 127.0f, s_lo = s_hi / 254.0f;
+      const float i_hi = am > 0.0f ? 127.0f / am : 0.0f, i_lo = am > 0.0f ? 254.0f * 127.0f / am : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float qh = fminf(fmaxf(rintf(xr[m][i] * i_hi), -127.0f), 127.0f);
+        const float rem = fmaf(-s_hi, qh, xr[m][i]);
+        const float ql = fminf(fmaxf(rintf(rem * i_lo), -127.0f), 127.0f);
+        const int d = 4 * lane + i, b = d >> 5, slot = q8_slot(b, d & 31);
+        qi[(r * 8 + b) * 32 + slot] = (uint8_t)(int8_t)qh;
+        qi[((r + 8) * 8 + b) * 32 + slot] = (uint8_t)(int8_t)ql;
+      }
+      if (lane == 0) {
+        sq[r] = s_hi * a.scale * kLog2e;
+        sq[r + 8] = s_lo * a.scale * kLog2e;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 8; ++b) qop[b] = *(const long *)(qi + (n * 8 + b) * 32 + 8 * g);
+    sqr = sq[n];
   } else {
     const int hh = n & 7;
     const bool on = hh < G;
@@ -684,7 +796,6 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const uint32_t sel_edge = g == 3 ? 0x05040302u : 0x07060504u;
   // pair mode: the last key of this lane's row; the P operand fills all 16 rows
   const int row_last = pair ? a.t + tok + (n >> 3) : t;
-  const uint32_t pmask = pair ? 0u : lo_mask;
 
   floatx4 o[16];
 #pragma unroll
@@ -715,13 +826,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       o[0][0] += sc[0] + sc[3];
       (void)vl;
     } else if constexpr (VT == F16) {
-#if RD4_DEC_PV_HILO
-      const half4 pf = __builtin_bit_cast(
-          half4, u32x2{split_prod2(sc[0], 1.0f, sc[1], 1.0f, lo_mask),
-                       split_prod2(sc[2], 1.0f, sc[3], 1.0f, lo_mask)});
-#else
-      const half4 pf = hi_only4(sc[0], sc[1], sc[2], sc[3], pmask);
-#endif
+      const half4 pf = p_op4(sc[0], sc[1], sc[2], sc[3]);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         // 16-byte chunk n + 16h (dims 8(n + 16h) .. +7) of the lane's 4 keys
@@ -747,14 +852,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
         const float4 dv = make_float4(dvs[b][0], dvs[b][1], dvs[b][2], dvs[b][3]);
-#if RD4_DEC_PV_HILO
-        const half4 pf = __builtin_bit_cast(
-            half4, u32x2{split_prod2(sc[0], dv.x, sc[1], dv.y, lo_mask),
-                         split_prod2(sc[2], dv.z, sc[3], dv.w, lo_mask)});
-#else
-        // P' = f16(p * d) in the hi rows, zero in the lo rows
-        const half4 pf = hi_only4(sc[0] * dv.x, sc[1] * dv.y, sc[2] * dv.z, sc[3] * dv.w, pmask);
-#endif
+        // P' = f16(p * d)
+        const half4 pf = p_op4(sc[0] * dv.x, sc[1] * dv.y, sc[2] * dv.z, sc[3] * dv.w);
         if constexpr (VT == Q4_1) {
           if (pair || n < 8) {
             const float4 mv = make_float4(mvs[b][0], mvs[b][1], mvs[b][2], mvs[b][3]);
@@ -870,7 +969,19 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         acc = floatx4{(float)lane, 1.f, 2.f, 3.f};
       } else {
         const uint8_t *krow = kl + n * KS;
-        if constexpr (KT == F16) {
+        if constexpr (kI8) {
+          floatx4 dks[8];
+          uint32_t kw[16], ke[4];
+          k_words_q8(krow, g, kw, ke);
+          tbl_read8(dk_t + 4 * g, dks);
+#pragma unroll
+          for (int b = 0; b < 8; ++b) {
+            const i32x4 z = {0, 0, 0, 0};
+            const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(k_op_i8(kw, ke, b, sel_edge), qop[b], z, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(dks[b][e], (float)c[e], acc[e]);
+          }
+        } else if constexpr (KT == F16) {
 #pragma unroll
           for (int b = 0; b < 8; ++b)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), q_frag(b), acc, 0, 0, 0);
@@ -907,7 +1018,13 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       const int lim = pair ? min(nk - 1, row_last - (j_begin + (w + i * kWaves) * kTile)) : nk - 1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float v = pair ? acc[i] * sl2 : (acc[i] + xor_f(acc[i], 8)) * sl2;
+        float v;
+        if constexpr (kI8) {
+          v = acc[i] * sqr;
+          v += xor_f(v, 8);
+        } else {
+          v = pair ? acc[i] * sl2 : (acc[i] + xor_f(acc[i], 8)) * sl2;
+        }
         if (4 * g + i > lim) v = -INFINITY;
         sc[i] = v;
         over |= v > m_run + kRescaleLog2;
@@ -947,21 +1064,22 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   {
     // o[t][i] holds dim v_dim<VT>(t, 4g + i); written back as 4-dim runs
     float *dst = wo + (w * 16 + n) * kRowPad;
+    const bool wr = pair || n < 8;  // single-token rows 8-15 duplicate rows 0-7
     if constexpr (VT == F16) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d0 = v_dim<VT>(8 * h, 4 * g + i);
-          *(floatx4 *)(dst + d0) = floatx4{o[8 * h][i], o[8 * h + 1][i], o[8 * h + 2][i], o[8 * h + 3][i]};
-          *(floatx4 *)(dst + d0 + 4) = floatx4{o[8 * h + 4][i], o[8 * h + 5][i], o[8 * h + 6][i], o[8 * h + 7][i]};
+          if (wr) *(floatx4 *)(dst + d0) = floatx4{o[8 * h][i], o[8 * h + 1][i], o[8 * h + 2][i], o[8 * h + 3][i]};
+          if (wr) *(floatx4 *)(dst + d0 + 4) = floatx4{o[8 * h + 4][i], o[8 * h + 5][i], o[8 * h + 6][i], o[8 * h + 7][i]};
         }
     } else if constexpr (VT == Q8_0) {
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
         const int d0 = v_dim<VT>(2 * b, 4 * g);
-        *(floatx4 *)(dst + d0) = floatx4{o[2 * b][0], o[2 * b + 1][0], o[2 * b][1], o[2 * b + 1][1]};
-        *(floatx4 *)(dst + d0 + 4) = floatx4{o[2 * b][2], o[2 * b + 1][2], o[2 * b][3], o[2 * b + 1][3]};
+        if (wr) *(floatx4 *)(dst + d0) = floatx4{o[2 * b][0], o[2 * b + 1][0], o[2 * b][1], o[2 * b + 1][1]};
+        if (wr) *(floatx4 *)(dst + d0 + 4) = floatx4{o[2 * b][2], o[2 * b + 1][2], o[2 * b][3], o[2 * b + 1][3]};
       }
     } else {
       if constexpr (VT == Q4_1) {
@@ -975,7 +1093,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       for (int t = 0; t < 16; ++t) {
         floatx4 v = o[t];
         if constexpr (VT == Q4_1) v += cm[t >> 1];
-        *(floatx4 *)(dst + v_dim<VT>(t, 4 * g)) = v;
+        if (wr) *(floatx4 *)(dst + v_dim<VT>(t, 4 * g)) = v;
       }
     }
   }
@@ -1014,7 +1132,6 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
 #pragma unroll
     for (int ww = 0; ww < kWaves; ++ww) {
       floatx4 ov = *(const floatx4 *)(wo + (ww * 16 + r) * kRowPad + d);
-      if (!pair) ov += *(const floatx4 *)(wo + (ww * 16 + hh + 8) * kRowPad + d);
       acc4 += ms[2 * kR + ww * kR + r] * ov;
     }
     const int64_t hrow_r = (int64_t)(tok + tr) * a.n_head + h0 + hh;
@@ -1089,7 +1206,7 @@ bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_d
          n_head % n_head_kv == 0;
 }
 
-bool decode_mfma_pairs(int kt, int vt) { return !RD4_DEC_PV_HILO && pair_type(kt, vt); }
+bool decode_mfma_pairs(int kt, int vt) { return pair_type(kt, vt); }
 
 bool decode_mfma_ext_merge() {
   // Split records are merged by a second, short launch: a kernel boundary makes
@@ -1110,7 +1227,7 @@ hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hip
   // pair mode needs host positions, f32 queries, no fused append and one head
   // chunk per kv head (the rows of two tokens share one 16-row tile)
   if (a.tok_pair && (a.pos || a.k_new || a.q_f16 || a.n_chunks != 1 || n_tok < 2 ||
-                     RD4_DEC_PV_HILO || !pair_type(kt, vt)))
+                     !pair_type(kt, vt)))
     a.tok_pair = 0;
   a.ext_merge = (a.n_splits > 1 && (a.tok_pair || decode_mfma_ext_merge())) ? 1 : 0;
   const int grid_tok = a.tok_pair ? (n_tok + 1) / 2 : n_tok;
