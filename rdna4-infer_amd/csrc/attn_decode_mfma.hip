@@ -565,7 +565,20 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   float *mk_t = dk_t + 128 * (iMK > 0 ? iMK : 0);
   float *mv_t = dk_t + 128 * (iMV > 0 ? iMV : 0);
   const int n_tiles_all = (j_end - j_begin + kTile - 1) / kTile;
-  const int my_tiles = (RD4_DEC_KNOBS && (a.dbg & 32)) ? 0 : (n_tiles_all > w ? (n_tiles_all - w + kWaves - 1) / kWaves : 0);
+  // Tile order: with 8 waves, waves w and w + 4 share a SIMD and the older one
+  // (w < 4) is issued first, so it takes more tiles: n_lo rounds go to all 8
+  // waves (tile 8i + w), the rest to waves 0-3 only (4 per round).
+#ifndef RD4_DEC_LO
+#define RD4_DEC_LO 6
+#endif
+  const int n_lo = kWaves == 8 ? n_tiles_all * RD4_DEC_LO / 64 : n_tiles_all;
+  const int t_rem = kWaves == 8 ? n_tiles_all - 8 * n_lo : 0;
+  const int my_tiles = (RD4_DEC_KNOBS && (a.dbg & 32)) ? 0
+                       : kWaves == 8 ? (w < 4 ? n_lo + (t_rem > w ? (t_rem - w + 3) / 4 : 0) : n_lo)
+                                     : (n_tiles_all > w ? (n_tiles_all - w + kWaves - 1) / kWaves : 0);
+  auto tile_of = [&](int i) {
+    return kWaves == 8 ? (i < n_lo ? 8 * i + w : 8 * n_lo + 4 * (i - n_lo) + w) : w + i * kWaves;
+  };
   // Global source of this lane's chunk in load instruction r of a tile:
   // byte offset from the tile's K (or V) base, with the f16 swizzle applied.
   // Rows past the tile's last key (partial tiles) re-read the tile's first row.
@@ -598,7 +611,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   }
   auto issue = [&](int i) {  // i-th tile of this wave
     if (RD4_DEC_KNOBS && (a.dbg & 2048)) return;
-    const int j0 = j_begin + (w + i * kWaves) * kTile;
+    const int j0 = j_begin + tile_of(i) * kTile;
     const int nk = min(kTile, j_end - j0);
     const uint8_t *kt0 = kbase + (int64_t)j0 * kstride;
     const uint8_t *vt0 = vbase + (int64_t)j0 * vstride;
@@ -931,7 +944,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     bool rescale_due = false;
     for (; i < my_tiles; ++i) {
       RD4_TP();
-      const int nk = min(kTile, j_end - (j_begin + (w + i * kWaves) * kTile));
+      const int j_tile = j_begin + tile_of(i) * kTile;
+      const int nk = min(kTile, j_end - j_tile);
       if (i + R - 1 < my_tiles) {
         // the stage being refilled was read by the previous iteration: those reads are done
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1015,7 +1029,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       bool over = false;
       // last key this lane's row may see, relative to the tile: pair mode masks the
       // second token's last key in the first token's rows
-      const int lim = pair ? min(nk - 1, row_last - (j_begin + (w + i * kWaves) * kTile)) : nk - 1;
+      const int lim = pair ? min(nk - 1, row_last - j_tile) : nk - 1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v;
