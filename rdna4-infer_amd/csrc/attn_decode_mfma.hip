@@ -68,6 +68,7 @@ constexpr int kRowPad = kHD + 4;  // LDS row stride (floats) of per-head rows: s
 constexpr int kTile = 16;    // keys per wave tile
 constexpr int kG = 8;        // query heads per CTA (MFMA rows 0-7 hi, 8-15 lo)
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kQiBytes = 16 * kHD + 64;  // int8 query rows [16][8 blocks][32] + 16 row scales
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ void wave_sync() {
@@ -124,7 +125,8 @@ struct TileShape {
 #define RD4_DEC_RMAX 3
 #endif
   static constexpr int WAVES = TB <= 10240 ? RD4_DEC_WAVES_SMALL : 4;
-  static constexpr int R0 = (152 * 1024 / WAVES - DT) / TB;
+  static constexpr int QI = KT == Q8_0 ? kQiBytes : 0;  // int8 query image (q8_0 K)
+  static constexpr int R0 = ((152 * 1024 - QI) / WAVES - DT) / TB;
   static constexpr int R = R0 < 2 ? 2 : (R0 > RD4_DEC_RMAX ? RD4_DEC_RMAX : R0);  // ring stages per wave
 };
 
@@ -183,6 +185,21 @@ __device__ __forceinline__ int q8_slot(int b, int e) {
   return e < 2 ? 28 + e : (e < 30 ? 24 + (e - 26) : 30 + (e - 30));
 }
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Max of a non-negative float over the 64 lanes of the wave, in every lane:
+// DPP steps within each 16-lane row (quad swaps, half-row and row mirrors), then
+// the row broadcasts carry the rows' maxima up to lane 63, read back as a
+// scalar. Non-negative floats order like their bit patterns.
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+  int v = __builtin_bit_cast(int, x);
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));  // row_mirror
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));  // row_bcast:15
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false));  // row_bcast:31
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 63));
+}
 
 // (x & m) | b in one VALU instruction (the compiler splits it into two
 // literal-operand ops; VOP3 on this target takes no literal, so m comes from
@@ -652,25 +669,29 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     }
   };
   if (!pair) issue_q();
+#ifndef RD4_DEC_PRE
+#define RD4_DEC_PRE 1
+#endif
+  // Tiles issued before the query rows have landed: one. The query rows gate
+  // the whole CTA, and more tile requests ahead of them (a chip-wide burst)
+  // delay them; the loop issues the rest of the ring at its start.
+  constexpr int kPre = RD4_DEC_PRE;
+  int next_issue = (RD4_DEC_PRE > 0 && !owns_new) ? min(kPre, my_tiles) : 0;  // next tile to issue
   if (!owns_new) {
 #pragma unroll
-    for (int i = 0; i < R - 1; ++i)
+    for (int i = 0; i < kPre; ++i)
       if (i < my_tiles) issue(i);  // first tiles in flight right behind the query rows
   }
   // this wave's query chunk has landed once at most the tile loads issued after it remain
   if (!pair) {
-    const int after = owns_new ? 0 : min(R - 1, my_tiles);
-    if (after >= 2) wait_vm<2 * NI>();
+    const int after = owns_new ? 0 : min(kPre, my_tiles);
+    if (after >= 3) wait_vm<3 * NI>();
+    else if (after == 2) wait_vm<2 * NI>();
     else if (after == 1) wait_vm<NI>();
     else wait_vm<0>();
     __syncthreads();
   }
   RD4_TP();
-  if (owns_new) {
-#pragma unroll
-    for (int i = 0; i < R - 1; ++i)
-      if (i < my_tiles) issue(i);
-  }
 
   // Query fragment (B operand of S^T = K Q^T): row n is head n (hi) or n-8
   // (lo); k-slot j of lane group g holds dim k_dim<KT>(b, g, j). Every wave
@@ -705,33 +726,36 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     }
   } else if constexpr (kI8) {
     // wave w quantizes head rows w, w + kWaves, ...: lane l holds dims 4l..4l+3;
-    // s_hi = amax / 127, q_hi = rint(q / s_hi), and the remainder on s_hi / 254
-    float xr[8 / kWaves][4];
+    // s_hi = amax / 127, q_hi = rint(q / s_hi), and the remainder on s_hi / 254.
+    // The int8 image lies past the query rows, so no barrier is needed before it.
+    uint8_t *qi = q_lds + kG * (kHD * 4 + 16) + 256;  // [16 rows][8 blocks][32 slots]
+    float *sq = (float *)(qi + 16 * kHD);              // [16] row scales (with scale * log2 e)
 #pragma unroll
     for (int m = 0; m < 8 / kWaves; ++m) {
       const int r = w + kWaves * m;
       const uint8_t *qrow = q_lds + (r < G ? r : 0) * qsb;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        xr[m][i] = r >= G ? 0.0f
-                   : a.q_f16 ? h2f(*(const uint16_t *)(qrow + 2 * (4 * lane + i)))
-                             : *(const float *)(qrow + 4 * (4 * lane + i));
-    }
-    __syncthreads();  // every wave has read the query rows
-    uint8_t *qi = q_lds;                          // [16 rows][8 blocks][4 g][8 bytes]
-    float *sq = (float *)(q_lds + 16 * kHD);      // [16] row scales (with scale * log2 e)
-#pragma unroll
-    for (int m = 0; m < 8 / kWaves; ++m) {
-      const int r = w + kWaves * m;
-      float am = fmaxf(fmaxf(fabsf(xr[m][0]), fabsf(xr[m][1])), fmaxf(fabsf(xr[m][2]), fabsf(xr[m][3])));
-#pragma unroll
-      for (int x = 1; x < 64; x <<= 1) am = fmaxf(am, xor_f(am, x));
+      float xr[4];
+      if (a.q_f16) {
+        const uint2 hv = *(const uint2 *)(qrow + 8 * lane);
+        xr[0] = h2f((uint16_t)hv.x);
+        xr[1] = h2f((uint16_t)(hv.x >> 16));
+        xr[2] = h2f((uint16_t)hv.y);
+        xr[3] = h2f((uint16_t)(hv.y >> 16));
+      } else {
+        const float4 fv = *(const float4 *)(qrow + 16 * lane);
+        xr[0] = fv.x;
+        xr[1] = fv.y;
+        xr[2] = fv.z;
+        xr[3] = fv.w;
+      }
+      if (r >= G) xr[0] = xr[1] = xr[2] = xr[3] = 0.0f;
+      const float am = wave_max_nonneg(fmaxf(fmaxf(fabsf(xr[0]), fabsf(xr[1])), fmaxf(fabsf(xr[2]), fabsf(xr[3]))));
       const float s_hi = am / 127.0f, s_lo = s_hi / 254.0f;
       const float i_hi = am > 0.0f ? 127.0f / am : 0.0f, i_lo = am > 0.0f ? 254.0f * 127.0f / am : 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float qh = fminf(fmaxf(rintf(xr[m][i] * i_hi), -127.0f), 127.0f);
-        const float rem = fmaf(-s_hi, qh, xr[m][i]);
+        const float qh = fminf(fmaxf(rintf(xr[i] * i_hi), -127.0f), 127.0f);
+        const float rem = fmaf(-s_hi, qh, xr[i]);
         const float ql = fminf(fmaxf(rintf(rem * i_lo), -127.0f), 127.0f);
         const int d = 4 * lane + i, b = d >> 5, slot = q8_slot(b, d & 31);
         qi[(r * 8 + b) * 32 + slot] = (uint8_t)(int8_t)qh;
@@ -946,10 +970,12 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       RD4_TP();
       const int j_tile = j_begin + tile_of(i) * kTile;
       const int nk = min(kTile, j_end - j_tile);
-      if (i + R - 1 < my_tiles) {
+      if (next_issue <= i + R - 1 && next_issue < my_tiles) {
         // the stage being refilled was read by the previous iteration: those reads are done
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        issue(i + R - 1);
+        do {
+          issue(next_issue++);
+        } while (next_issue <= i + R - 1 && next_issue < my_tiles);
       }
       // tile i is complete once at most the loads of the tiles issued after it remain
       const int after = min(R - 1, my_tiles - 1 - i);
@@ -1187,7 +1213,7 @@ template <int KT, int VT>
 size_t decode_lds() {
   using TS = TileShape<KT, VT>;
   // query rows (later the shared fragments and the q4_1 block sums)
-  const size_t qreg = (size_t)kG * (kHD * 4 + 16) + 256;
+  const size_t qreg = (size_t)kG * (kHD * 4 + 16) + 256 + TS::QI;
   const size_t tiles = (size_t)TS::WAVES * TS::R * TS::TB + qreg;  // scale tables are static LDS
   const size_t merge = (2 * TS::WAVES * 16 + TS::WAVES * 16 * kRowPad + 2 * 16 + TS::WAVES * 16 + 4) * 4 +
                        (kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
