@@ -68,7 +68,7 @@ constexpr int kRowPad = kHD + 4;  // LDS row stride (floats) of per-head rows: s
 constexpr int kTile = 16;    // keys per wave tile
 constexpr int kG = 8;        // query heads per CTA (MFMA rows 0-7 hi, 8-15 lo)
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kQiBytes = 16 * kHD + 64;  // int8 query rows [16][8 blocks][32] + 16 row scales
+constexpr int kQiBytes = 16 * kHD + 16 * 8 * 4;  // int8 query rows [16][8 blocks][32] + scales [16][8]
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ void wave_sync() {
@@ -186,19 +186,15 @@ __device__ __forceinline__ int q8_slot(int b, int e) {
 }
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-// Max of a non-negative float over the 64 lanes of the wave, in every lane:
-// DPP steps within each 16-lane row (quad swaps, half-row and row mirrors), then
-// the row broadcasts carry the rows' maxima up to lane 63, read back as a
-// scalar. Non-negative floats order like their bit patterns.
-__device__ __forceinline__ float wave_max_nonneg(float x) {
+// Max of a non-negative float over each group of 8 lanes (8k .. 8k + 7), in
+// every lane of the group: DPP quad swaps and the half-row mirror.
+// Non-negative floats order like their bit patterns.
+__device__ __forceinline__ float max8_nonneg(float x) {
   int v = __builtin_bit_cast(int, x);
   v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
   v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
   v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));  // row_half_mirror
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));  // row_mirror
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));  // row_bcast:15
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false));  // row_bcast:31
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 63));
+  return __builtin_bit_cast(float, v);
 }
 
 // (x & m) | b in one VALU instruction (the compiler splits it into two
@@ -498,7 +494,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   constexpr int TB = TS::TB, R = TS::R, DT = TS::DT;
 
   // q8_0 K in single-token mode: S^T on the int8 MFMA, the query as int8 hi and
-  // lo rows (q = s_hi q_hi + s_lo q_lo to ~amax / 65000 per row)
+  // lo rows with a scale pair per 32-dim block (q = s_hi q_hi + s_lo q_lo to
+  // ~amax / 65000 of the block)
   constexpr bool kI8 = KT == Q8_0 && !PAIR;
   const int s = blockIdx.x;
   const int kvh = blockIdx.y / a.n_chunks;
@@ -700,8 +697,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const uint32_t lo_mask = n >= 8 ? 0xffffffffu : 0u;
   half8 qf[8];
   float qblk[8];
-  long qop[kI8 ? 8 : 1];  // int8 query fragments (kI8)
-  float sqr = 0.0f;       // this lane's row scale (kI8)
+  long qop[kI8 ? 8 : 1];    // int8 query fragments (kI8)
+  float sqb[kI8 ? 8 : 1];   // this lane's row scale per block (kI8)
   if (pair) {
     // f16 query rows straight from global memory, both tokens' heads
     const int hh = n & 7, tr = n >> 3;
@@ -725,11 +722,12 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       }
     }
   } else if constexpr (kI8) {
-    // wave w quantizes head rows w, w + kWaves, ...: lane l holds dims 4l..4l+3;
-    // s_hi = amax / 127, q_hi = rint(q / s_hi), and the remainder on s_hi / 254.
-    // The int8 image lies past the query rows, so no barrier is needed before it.
+    // wave w quantizes head rows w, w + kWaves, ...: lane l holds dims 4l..4l+3
+    // of block l / 8; per block s_hi = amax / 127, q_hi = rint(q / s_hi), and the
+    // remainder on s_hi / 254. The int8 image lies past the query rows, so no
+    // barrier is needed before it.
     uint8_t *qi = q_lds + kG * (kHD * 4 + 16) + 256;  // [16 rows][8 blocks][32 slots]
-    float *sq = (float *)(qi + 16 * kHD);              // [16] row scales (with scale * log2 e)
+    float *sq = (float *)(qi + 16 * kHD);              // [16 rows][8 blocks] scales (with scale * log2 e)
 #pragma unroll
     for (int m = 0; m < 8 / kWaves; ++m) {
       const int r = w + kWaves * m;
@@ -749,7 +747,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         xr[3] = fv.w;
       }
       if (r >= G) xr[0] = xr[1] = xr[2] = xr[3] = 0.0f;
-      const float am = wave_max_nonneg(fmaxf(fmaxf(fabsf(xr[0]), fabsf(xr[1])), fmaxf(fabsf(xr[2]), fabsf(xr[3]))));
+      const float am = max8_nonneg(fmaxf(fmaxf(fabsf(xr[0]), fabsf(xr[1])), fmaxf(fabsf(xr[2]), fabsf(xr[3]))));
       const float s_hi = am / 127.0f, s_lo = s_hi / 254.0f;
       const float i_hi = am > 0.0f ? 127.0f / am : 0.0f, i_lo = am > 0.0f ? 254.0f * 127.0f / am : 0.0f;
 #pragma unroll
@@ -761,15 +759,17 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         qi[(r * 8 + b) * 32 + slot] = (uint8_t)(int8_t)qh;
         qi[((r + 8) * 8 + b) * 32 + slot] = (uint8_t)(int8_t)ql;
       }
-      if (lane == 0) {
-        sq[r] = s_hi * a.scale * kLog2e;
-        sq[r + 8] = s_lo * a.scale * kLog2e;
+      if ((lane & 7) == 0) {
+        sq[r * 8 + (lane >> 3)] = s_hi * a.scale * kLog2e;
+        sq[(r + 8) * 8 + (lane >> 3)] = s_lo * a.scale * kLog2e;
       }
     }
     __syncthreads();
 #pragma unroll
-    for (int b = 0; b < 8; ++b) qop[b] = *(const long *)(qi + (n * 8 + b) * 32 + 8 * g);
-    sqr = sq[n];
+    for (int b = 0; b < 8; ++b) {
+      qop[b] = *(const long *)(qi + (n * 8 + b) * 32 + 8 * g);
+      sqb[b] = sq[n * 8 + b];
+    }
   } else {
     const int hh = n & 7;
     const bool on = hh < G;
@@ -1019,7 +1019,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
             const i32x4 z = {0, 0, 0, 0};
             const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(k_op_i8(kw, ke, b, sel_edge), qop[b], z, 0, 0, 0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = fmaf(dks[b][e], (float)c[e], acc[e]);
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(dks[b][e], (float)c[e] * sqb[b], acc[e]);
           }
         } else if constexpr (KT == F16) {
 #pragma unroll
@@ -1060,8 +1060,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       for (int i = 0; i < 4; ++i) {
         float v;
         if constexpr (kI8) {
-          v = acc[i] * sqr;
-          v += xor_f(v, 8);
+          v = acc[i] + xor_f(acc[i], 8);
         } else {
           v = pair ? acc[i] * sl2 : (acc[i] + xor_f(acc[i], 8)) * sl2;
         }

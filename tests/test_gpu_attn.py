@@ -54,6 +54,28 @@ def test_all_36_pairs(rd4, orc, dev, kt, vt):
     check_close(got, want, "pair %d/%d" % (kt, vt))
 
 
+@pytest.mark.parametrize("kt,vt", [(2, 2), (2, 3), (3, 3), (1, 1), (5, 4)])
+def test_query_outlier_dims(rd4, orc, dev, kt, vt):
+    """Queries with a wide dynamic range: one dim x100 in every head, one head of
+    values ~1e-3 with a single dim of 50, one all-zero head. The q8_0 K path
+    carries the f32 query as int8 hi/lo parts with a scale pair per 32-dim block,
+    so a large dim coarsens only its own block."""
+    import torch
+    nh, nkv, hd, n = 24, 4, 256, 700
+    k = make_cache(orc, kt, n, nkv, hd, 50 + kt, outlier=True)
+    v = make_cache(orc, vt, n, nkv, hd, 60 + vt)
+    q = orc.randn(nh * hd, 61).reshape(nh, hd)
+    q[:, 7] *= 100.0
+    q[3] *= 1e-3
+    q[3, 200] = 50.0
+    q[5] = 0.0
+    q = np.ascontiguousarray(q.ravel())
+    want = orc.attn_decode(q, k, v, n - 1, nh, nkv, hd, 1 / 16, kt, vt)
+    for splits in (1, 0):
+        got, _ = run_decode(rd4, torch, dev, q, k, v, n - 1, nh, nkv, hd, kt, vt, n_splits=splits)
+        check_close(got, want, "outlier q %d/%d splits %d" % (kt, vt, splits))
+
+
 @pytest.mark.parametrize("splits", [1, 2, 7, 16, 17, 64, 256])
 def test_split_invariance_and_merge_tree(rd4, orc, dev, splits):
     """Any split count (one-level merge <= 16, two-level above) gives the same
