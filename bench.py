@@ -156,7 +156,7 @@ def tokens_workload(torch, rd4, kt=2, ctx=32768, n_tok=4):
 def prefill_workload(torch, rd4, n_prefix=4096, n_q=4096):
     """4096 f16 queries at positions 4096..8191 over an f16 cache of
     8192 rows (prefix + the chunk), causal, gated; the chunk's K/V rows are also
-    appended to a q8_0 cache in the same step."""
+    appended to a q8_0 cache in the same launch (rd4_prefill_append)."""
     ktot = n_prefix + n_q
     kc = make_cache(torch, rd4, 1, ktot, SEED, False)
     vc = make_cache(torch, rd4, 1, ktot, SEED + 1, False)
@@ -172,13 +172,13 @@ def prefill_workload(torch, rd4, n_prefix=4096, n_q=4096):
     pairs = n_q * (n_prefix + 1) + n_q * (n_q - 1) // 2
     flops = NH * pairs * 4 * HD
 
-    def attn():
-        rd4.prefill(q, kc, vc, out, n_prefix, NH, NKV, HD, 1.0 / 16, 1, 1, gate=gate)
+    kq8_chunk, vq8_chunk = kq8[n_prefix * NKV * rb8:], vq8[n_prefix * NKV * rb8:]
 
     def step():
-        rd4.kv_store_rows(2, knew, kq8[n_prefix * NKV * rb8:])
-        rd4.kv_store_rows(2, vnew, vq8[n_prefix * NKV * rb8:])
-        attn()
+        # one launch: gated causal prefill + the chunk's K/V rows appended as q8_0
+        rd4.prefill_append(q, kc, vc, out, n_prefix, NH, NKV, HD, 1.0 / 16, 1, 1, knew, vnew,
+                           kq8_chunk, vq8_chunk, 2, gate=gate)
+    attn = step
 
     def cpu(budget_s=12.0):
         """Oracle on a deterministic subset of query rows, scaled by causal pairs."""

@@ -194,6 +194,20 @@ int rd4_prefill(const void *q, int q_f16, const void *k, const void *v, float *o
                 int pos0, int n_q, int n_head, int n_head_kv, int head_dim, float scale, int kt,
                 int vt, void *stream);
 
+/* Prefill with the chunk's K/V append fused into the same launch: the store of
+ * graph.cuh:1462 (kv_write_batch -> kv_store_row_launch over the chunk's rows,
+ * graph.cuh:1011-1031, kv.h:683) and the prefill + gate of graph.cuh:1479-1535
+ * in one pass. k_new / v_new are f32
+ * [n_q][n_head_kv][head_dim]; their rows are quantized to dst_type into k_dst /
+ * v_dst (rows contiguous, the chunk's first row at the pointer), byte-identical to
+ * rd4_kv_store_row_launch. The destination must not overlap the attended rows
+ * 0..pos0+n_q-1 of k or v (the launch reads them while it writes): RD4_EINVAL.
+ * Shapes the MFMA kernel does not take run the store launches then the prefill. */
+int rd4_prefill_append(const void *q, int q_f16, const void *k, const void *v, float *out,
+                       float *gate, int pos0, int n_q, int n_head, int n_head_kv, int head_dim,
+                       float scale, int kt, int vt, const float *k_new, const float *v_new,
+                       void *k_dst, void *v_dst, int dst_type, void *stream);
+
 /* ---- gate / rope ---------------------------------------------------------- */
 
 /* sigmoid_gate_launch (nn.cuh:414): g <- sigmoid(g); y <- y * g. */

@@ -44,6 +44,8 @@ SIGNATURES = {
     "rd4_fa2_prefill_launch": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
     "rd4_fa2_prefill_usable": ([_I, _I, _I, _I, _I, _I, _I], _I),
     "rd4_prefill": ([_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I),
+    "rd4_prefill_append": ([_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P, _P, _P, _I,
+                            _P], _I),
     "rd4_sigmoid_gate_launch": ([_P, _P, _I64, _P], _I),
     "rd4_rope_launch": ([_P, _I, _I, _I, _I, _F, _P, _P], _I),
     "rd4_attn_decode_tokens": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
@@ -200,6 +202,18 @@ def prefill(q, k, v, out, pos0, n_head, n_head_kv, head_dim, scale, kt, vt, gate
     _check(lib().rd4_prefill(_ptr(q), q_f16, _ptr(k), _ptr(v), _ptr(out), _ptr(gate), pos0,
                              q.shape[0], n_head, n_head_kv, head_dim, scale, kt, vt, _stream()),
            "prefill")
+
+
+def prefill_append(q, k, v, out, pos0, n_head, n_head_kv, head_dim, scale, kt, vt, k_new, v_new,
+                   k_dst, v_dst, dst_type, gate=None):
+    """prefill() with the chunk's new K/V rows (f32 [n_q][n_head_kv][hd]) quantized to
+    dst_type into k_dst / v_dst in the same launch (graph.cuh:1462 store + 1479-1535)."""
+    import torch
+    q_f16 = 1 if q.dtype == torch.float16 else 0
+    _check(lib().rd4_prefill_append(_ptr(q), q_f16, _ptr(k), _ptr(v), _ptr(out), _ptr(gate), pos0,
+                                    q.shape[0], n_head, n_head_kv, head_dim, scale, kt, vt,
+                                    _ptr(k_new), _ptr(v_new), _ptr(k_dst), _ptr(v_dst), dst_type,
+                                    _stream()), "prefill_append")
 
 
 def fa2_prefill(q, k, v, out, pos, kmax, keys_total, n_head, n_head_kv, head_dim, scale):

@@ -29,6 +29,7 @@
 // Row blocks are scheduled heaviest (latest queries) first.
 #include <cstdlib>
 
+#include "kv_quant.hpp"
 #include "prefill.hpp"
 
 namespace rd4 {
@@ -84,6 +85,29 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   }
   const int rb = n_rb - 1 - rbp;
   const int r0 = rb * kBM;
+
+  // Fused append: the chunk's new K and V rows (2 * n_q * n_head_kv of them) are
+  // spread over the CTAs, one wave per row, 8 lanes per 32-value block, with the
+  // quantizer of kv_store_row_launch; the attention below reads other rows.
+  if (p.app_k) {
+    const int nrow = p.n_q * p.n_head_kv, total_rows = 2 * nrow;
+    const int rb_bytes = (int)row_bytes(p.app_type, kHD);
+    for (int R = (int)blockIdx.x * kWaves + w; R < total_rows; R += (int)gridDim.x * kWaves) {
+      const bool isv = R >= nrow;
+      const int rr = isv ? R - nrow : R;
+      const float4 x4 = *(const float4 *)((isv ? p.app_v_src : p.app_k_src) + (int64_t)rr * kHD + 4 * lane);
+      const float x[4] = {x4.x, x4.y, x4.z, x4.w};
+      uint8_t *row = (isv ? p.app_v : p.app_k) + (int64_t)rr * rb_bytes;
+      switch (p.app_type) {
+        case F32: store_group4<F32>(x, lane & 7, row, lane >> 3); break;
+        case F16: store_group4<F16>(x, lane & 7, row, lane >> 3); break;
+        case Q8_0: store_group4<Q8_0>(x, lane & 7, row, lane >> 3); break;
+        case Q4_0: store_group4<Q4_0>(x, lane & 7, row, lane >> 3); break;
+        case Q5_0: store_group4<Q5_0>(x, lane & 7, row, lane >> 3); break;
+        default: store_group4<Q4_1>(x, lane & 7, row, lane >> 3); break;
+      }
+    }
+  }
 
   // Causal limit of a row: last key it may attend.
   auto limit_of = [&](int row) -> int {

@@ -430,6 +430,60 @@ int rd4_prefill(const void *q, int q_f16, const void *k, const void *v, float *o
   return launched(prefill_launch(kt, vt, p, (hipStream_t)stream), "prefill");
 }
 
+int rd4_prefill_append(const void *q, int q_f16, const void *k, const void *v, float *out,
+                       float *gate, int pos0, int n_q, int n_head, int n_head_kv, int head_dim,
+                       float scale, int kt, int vt, const float *k_new, const float *v_new,
+                       void *k_dst, void *v_dst, int dst_type, void *stream) {
+  if (n_q < 1 || pos0 < 0 || !q || !k || !v || !out) return fail(RD4_EINVAL, "bad prefill shape%s");
+  int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
+  if (rc) return rc;
+  if (!valid_type(dst_type)) return fail(RD4_ETYPE, "KvType outside the enum%s");
+  if (!k_new || !v_new || !k_dst || !v_dst) return fail(RD4_EINVAL, "null append buffer%s");
+  // The fused append writes while the attention reads: the destination rows must
+  // lie outside the attended rows 0 .. pos0 + n_q - 1 of either cache.
+  const int64_t app = (int64_t)n_q * n_head_kv * row_bytes(dst_type, head_dim);
+  const int64_t att_k = (int64_t)(pos0 + n_q) * n_head_kv * row_bytes(kt, head_dim);
+  const int64_t att_v = (int64_t)(pos0 + n_q) * n_head_kv * row_bytes(vt, head_dim);
+  auto overlap = [](const void *a, int64_t na, const void *b, int64_t nb) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + (uintptr_t)nb && y < x + (uintptr_t)na;
+  };
+  if (overlap(k_dst, app, k, att_k) || overlap(k_dst, app, v, att_v) || overlap(v_dst, app, k, att_k) ||
+      overlap(v_dst, app, v, att_v) || overlap(k_dst, app, v_dst, app))
+    return fail(RD4_EINVAL, "append destination overlaps the attended cache rows%s");
+  const bool mfma = ((((uintptr_t)q) | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)gate |
+                      (uintptr_t)k_new | (uintptr_t)v_new) & 15) == 0 &&
+                    prefill_mfma_supported(kt, vt, n_head, n_head_kv, head_dim);
+  if (!mfma) {  // other shapes: the store launch, then the prefill launch, on the same stream
+    if ((rc = rd4_kv_store_row_launch(dst_type, k_new, k_dst, (int64_t)n_q * n_head_kv * head_dim, stream)))
+      return rc;
+    if ((rc = rd4_kv_store_row_launch(dst_type, v_new, v_dst, (int64_t)n_q * n_head_kv * head_dim, stream)))
+      return rc;
+    return rd4_prefill(q, q_f16, k, v, out, gate, pos0, n_q, n_head, n_head_kv, head_dim, scale, kt, vt,
+                       stream);
+  }
+  PrefillArgs p{};
+  p.q = q;
+  p.q_f16 = q_f16 ? 1 : 0;
+  p.k = (const uint8_t *)k;
+  p.v = (const uint8_t *)v;
+  p.out = out;
+  p.gate = gate;
+  p.pos0 = pos0;
+  p.kmax = pos0 + n_q - 1;
+  p.n_q = n_q;
+  p.n_head = n_head;
+  p.n_head_kv = n_head_kv;
+  p.head_dim = head_dim;
+  p.scale = scale;
+  p.app_k_src = k_new;
+  p.app_v_src = v_new;
+  p.app_k = (uint8_t *)k_dst;
+  p.app_v = (uint8_t *)v_dst;
+  p.app_type = dst_type;
+  return launched(prefill_launch(kt, vt, p, (hipStream_t)stream), "prefill");
+}
+
 int rd4_sigmoid_gate_launch(float *g_io, float *y_io, int64_t n, void *stream) {
   if (n < 0 || (n > 0 && (!g_io || !y_io))) return fail(RD4_EINVAL, "bad gate buffers%s");
   return launched(sigmoid_gate_launch(g_io, y_io, n, (hipStream_t)stream), "sigmoid gate");

@@ -16,6 +16,12 @@ struct PrefillArgs {
   int n_q, n_head, n_head_kv, head_dim;
   float scale;
   int dbg;  // profiling knob bits (0 in production)
+  // Optional append fused into the same launch: the chunk's new K/V rows, f32
+  // [n_q][n_head_kv][hd] each, quantized to app_type into app_k / app_v (rows
+  // contiguous, the chunk's first row at the pointer), as kv_store_row_launch.
+  const float *app_k_src, *app_v_src;
+  uint8_t *app_k, *app_v;
+  int app_type;
 };
 
 bool prefill_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim);

@@ -108,3 +108,55 @@ def test_prefill_mfma_matches_generic(rd4, orc, dev, monkeypatch):
     monkeypatch.setenv("RD4_PREFILL_GENERIC", "1")
     rd4.prefill(q, k, v, b, pos0, nh, nkv, hd, 1 / 16, 1, 1)
     check_close(a.cpu().numpy(), b.cpu().numpy(), "mfma vs generic")
+
+
+@pytest.mark.parametrize("dst_type,q_f16", [(2, True), (3, False), (1, True), (4, True), (5, True), (0, True)])
+def test_prefill_append_fused(rd4, orc, dev, dst_type, q_f16):
+    """rd4_prefill_append: the chunk's K/V rows quantized into a second cache in
+    the same launch. The attention output and gate equal rd4_prefill's bit for bit;
+    the appended bytes equal the oracle's quantization of the same rows."""
+    import torch
+    nh, nkv, hd, pos0, nq = 24, 4, 256, 200, 300
+    n = pos0 + nq
+    k = to_dev(orc.store_rows(1, orc.randn(n * nkv * hd, 21)), torch, dev)
+    v = to_dev(orc.store_rows(1, orc.randn(n * nkv * hd, 22)), torch, dev)
+    q = orc.randn(nq * nh * hd, 23).reshape(nq, nh, hd)
+    qd = to_dev(q.astype(np.float16) if q_f16 else q, torch, dev)
+    g = orc.randn(nq * nh * hd, 24)
+    knew = orc.randn(nq * nkv * hd, 25)
+    vnew = orc.randn(nq * nkv * hd, 26)
+    knew[7 * hd + 3] = 0.0
+    vnew[: hd] *= 40.0  # a wide row
+    rb = rd4.kv_row_bytes(dst_type, hd)
+    kdst = torch.zeros(n * nkv * rb, dtype=torch.uint8, device=dev)
+    vdst = torch.zeros(n * nkv * rb, dtype=torch.uint8, device=dev)
+    off = pos0 * nkv * rb
+    out1 = torch.empty(nq * nh * hd, dtype=torch.float32, device=dev)
+    g1 = to_dev(g, torch, dev)
+    rd4.prefill_append(qd, k, v, out1, pos0, nh, nkv, hd, 1 / 16, 1, 1, to_dev(knew, torch, dev),
+                       to_dev(vnew, torch, dev), kdst[off:], vdst[off:], dst_type, gate=g1)
+    out0 = torch.empty_like(out1)
+    g0 = to_dev(g, torch, dev)
+    rd4.prefill(qd, k, v, out0, pos0, nh, nkv, hd, 1 / 16, 1, 1, gate=g0)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out0) and torch.equal(g1, g0)
+    assert np.array_equal(kdst[off:].cpu().numpy(), orc.store_rows(dst_type, knew))
+    assert np.array_equal(vdst[off:].cpu().numpy(), orc.store_rows(dst_type, vnew))
+    assert not kdst[:off].any() and not vdst[:off].any()
+
+
+def test_prefill_append_rejects_overlap(rd4, orc, dev):
+    """Appending into the rows the same launch attends is refused (the reference
+    stores first, then attends; one pass cannot order that)."""
+    import torch
+    nh, nkv, hd, pos0, nq = 24, 4, 256, 64, 32
+    n = pos0 + nq
+    rb = rd4.kv_row_bytes(1, hd)
+    k = torch.zeros(n * nkv * rb, dtype=torch.uint8, device=dev)
+    v = torch.zeros_like(k)
+    q = torch.zeros(nq * nh * hd, dtype=torch.float16, device=dev).reshape(nq, nh, hd)
+    out = torch.empty(nq * nh * hd, dtype=torch.float32, device=dev)
+    src = torch.zeros(nq * nkv * hd, dtype=torch.float32, device=dev)
+    with pytest.raises(rd4.Rd4Error):
+        rd4.prefill_append(q, k, v, out, pos0, nh, nkv, hd, 1 / 16, 1, 1, src, src,
+                           k[pos0 * nkv * rb:], v[pos0 * nkv * rb:], 1)
