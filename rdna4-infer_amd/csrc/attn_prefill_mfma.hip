@@ -63,7 +63,9 @@ __device__ __forceinline__ _Float16 h16(uint16_t b) { return __builtin_bit_cast(
 
 __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p) {
   extern __shared__ __align__(16) uint8_t smem[];
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // the wave index is uniform: readfirstlane keeps DMA bases and LDS
+  // destinations in scalar registers
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
   const int grp = p.n_head / p.n_head_kv;
   const int n_rows = p.n_q * grp;
@@ -197,12 +199,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   // ---- block loads. K: 2048 chunks of 16 B per block = 8 DMA instructions per
   // lane; chunk c -> key c/32, LDS slot c%32 holds global column slot^(key&15).
   // Per-lane offsets are block-invariant and computed once.
-  int k_goff[kNDMA];  // byte offset of this lane's chunk r from the block's first key
+  uint32_t k_goff[kNDMA];  // byte offset of this lane's chunk r from the block's first key (scalar base + 32-bit vector offset)
 #pragma unroll
   for (int r = 0; r < kNDMA; ++r) {
     const int c = (w * kNDMA + r) * 64 + lane;
     const int key = c >> 5, slot = c & 31;
-    k_goff[r] = key * (int)kvstride + 16 * (slot ^ (key & 15));
+    k_goff[r] = (uint32_t)(key * (int)kvstride + 16 * (slot ^ (key & 15)));
   }
   auto issue_k = [&](int blk, int stage) {
     uint8_t *kd = smem + stage * kKBytes;
