@@ -53,8 +53,10 @@ constexpr int kNDMA = 2048 / (64 * kWaves); // 16-byte DMA chunks per lane per K
 constexpr int kBM = kWaves * kRowsW;       // rows per CTA
 constexpr int kBN = 64;                    // keys per block
 constexpr int kKBytes = kBN * kHD * 2;     // K block, 32 KiB
-// LDS: two K stages then two V stages
-constexpr int kLdsBytes = 4 * kKBytes;
+// LDS: three K stages then two V stages (the whole 160 KiB): K streams two
+// blocks ahead, V one
+constexpr int kKStages = 3, kVStages = 2;
+constexpr int kLdsBytes = (kKStages + kVStages) * kKBytes;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ _Float16 h16(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
@@ -118,19 +120,16 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
     const int lp = p.pos ? p.pos[q] : p.pos0 + q;
     return min(lp, p.kmax);
   };
-  // Key range of the CTA: 0 .. max limit over its rows.
-  __shared__ int s_kend;
-  if (tid == 0) s_kend = -1;
-  __syncthreads();
+  // Key range of the CTA: 0 .. max limit over its rows, reduced by every wave
+  // over all of the CTA's rows (no LDS: the K/V stages take all of it).
+  int kend;  // inclusive
   {
     int lim = -1;
-    for (int r = tid; r < kBM; r += kThreads) lim = max(lim, limit_of(r0 + r));
+    for (int r = lane; r < kBM; r += 64) lim = max(lim, limit_of(r0 + r));
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) lim = max(lim, __shfl_xor(lim, m, 64));
-    if (lane == 0) atomicMax(&s_kend, lim);
+    kend = __builtin_amdgcn_readfirstlane(lim);
   }
-  __syncthreads();
-  const int kend = s_kend;  // inclusive
   const int n_blocks = (kend + kBN) / kBN;
 
   const int64_t kvstride = (int64_t)p.n_head_kv * kHD * 2;  // bytes between consecutive keys
@@ -227,9 +226,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
       }
     }
   };
-  // V: same DMA and swizzle as K, into its own two stages.
+  // V: same DMA and swizzle as K, into its own stages.
   auto issue_v = [&](int blk, int stage) {
-    uint8_t *vd = smem + (2 + stage) * kKBytes;
+    uint8_t *vd = smem + (kKStages + stage) * kKBytes;
     const int j0 = blk * kBN;
     const uint8_t *src = vbase + (int64_t)j0 * kvstride;
     if (j0 + kBN - 1 <= kend) {
@@ -262,21 +261,29 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 #pragma unroll
   for (int b = 0; b < 8; ++b) k_loff[b] = n * (kHD * 2) + 64 * (b ^ (n >> 2)) + 16 * (g ^ (n & 3));
 
+  // Issue order: K0 V0 K1, then in block j: V(j+1), K(j+2). At the top of block
+  // j the loads issued after V(j) are K(j+1)'s only, so waiting until at most
+  // those remain lands K(j) and V(j) and leaves K(j+1) in flight.
   if (n_blocks > 0) {
     issue_k(0, 0);
     issue_v(0, 0);
   }
+  if (n_blocks > 1) issue_k(1, 1);
+  int ks = 0;  // K stage of the current block (blk % 3)
   for (int blk = 0; blk < n_blocks; ++blk) {
-    const int st = blk & 1;
-    const bool more = blk + 1 < n_blocks;
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA for blk landed
-    __syncthreads();  // every wave's DMA for blk landed; every wave is done with blk - 1
-    if (more) {
-      issue_k(blk + 1, st ^ 1);
-      issue_v(blk + 1, st ^ 1);
+    const int vs = blk & 1;
+    if (blk + 1 < n_blocks) {
+      static_assert(kNDMA == 4, "vmcnt below counts one K block's DMA instructions");
+      __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");  // K(j), V(j) landed; K(j+1) may fly
+    } else {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    const uint8_t *kd = smem + st * kKBytes;
-    const uint8_t *vd = smem + (2 + st) * kKBytes;
+    __syncthreads();  // every wave's DMA for blk landed; every wave is done with blk - 1
+    if (blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
+    if (blk + 2 < n_blocks) issue_k(blk + 2, ks == 0 ? 2 : ks - 1);  // (blk + 2) % 3
+    const uint8_t *kd = smem + ks * kKBytes;
+    const uint8_t *vd = smem + (kKStages + vs) * kKBytes;
+    ks = ks == 2 ? 0 : ks + 1;
     const int j0 = blk * kBN;
     const bool need_mask = (j0 + kBN - 1) > wave_min_lim;
 
