@@ -456,6 +456,28 @@ __device__ __forceinline__ void tbl_read8(const float *p, floatx4 (&out)[8]) {
       : "v"(a)
       : "memory");
 }
+// tbl_read8 plus the two float4 at q (8 consecutive floats), in one batch.
+__device__ __forceinline__ void tbl_read8_q2(const float *p, const float *q, floatx4 (&out)[8], floatx4 &q0,
+                                             floatx4 &q1) {
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)p;
+  const uint32_t b = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)q;
+  __asm__ volatile(
+      "ds_read_b128 %0, %10\n\t"
+      "ds_read_b128 %1, %10 offset:64\n\t"
+      "ds_read_b128 %2, %10 offset:128\n\t"
+      "ds_read_b128 %3, %10 offset:192\n\t"
+      "ds_read_b128 %4, %10 offset:256\n\t"
+      "ds_read_b128 %5, %10 offset:320\n\t"
+      "ds_read_b128 %6, %10 offset:384\n\t"
+      "ds_read_b128 %7, %10 offset:448\n\t"
+      "ds_read_b128 %8, %11\n\t"
+      "ds_read_b128 %9, %11 offset:16\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(out[4]), "=&v"(out[5]),
+        "=&v"(out[6]), "=&v"(out[7]), "=&v"(q0), "=&v"(q1)
+      : "v"(a), "v"(b)
+      : "memory");
+}
 // f16 of four products, the B operand of one PV MFMA. In single-token mode
 // rows n and n + 8 carry the same head (the hi and lo query parts were summed
 // into both), so their O columns come out identical and rows 8-15 are ignored.
@@ -698,7 +720,10 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   half8 qf[8];
   float qblk[8];
   long qop[kI8 ? 8 : 1];    // int8 query fragments (kI8)
-  float sqb[kI8 ? 8 : 1];   // this lane's row scale per block (kI8)
+  // this lane's row scale per block (kI8); with q4_1 V (more live registers in
+  // the tile loop) they are re-read from LDS with the K scale table instead
+  constexpr bool kSqReg = VT != Q4_1;
+  float sqb[kI8 && kSqReg ? 8 : 1];
   if (pair) {
     // f16 query rows straight from global memory, both tokens' heads
     const int hh = n & 7, tr = n >> 3;
@@ -768,7 +793,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       qop[b] = *(const long *)(qi + (n * 8 + b) * 32 + 8 * g);
-      sqb[b] = sq[n * 8 + b];
+      if constexpr (kSqReg) sqb[b] = sq[n * 8 + b];
     }
   } else {
     const int hh = n & 7;
@@ -884,6 +909,20 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       }
     } else {
       floatx4 dvs[8], mvs[VT == Q4_1 ? 8 : 1];
+      // the V bytes of the lane's 4 keys for all 8 blocks are read ahead of the
+      // scale table, whose asm batch then lands them in the same round trip
+      // (q5_0 and q4_1, with more live registers here, read per block below)
+      constexpr bool kHoistV = VT == Q8_0 || VT == Q4_0;
+      uint32_t ur[kHoistV ? 8 : 1][4];
+      if constexpr (kHoistV) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint8_t *vrow = vl + (4 * g + i) * VS + block_bytes(VT) * b + (VT == Q4_1 ? 4 : 2);
+            ur[b][i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
+          }
+      }
       tbl_read8(dv_t + 4 * g, dvs);
       if constexpr (VT == Q4_1) tbl_read8(mv_t + 4 * g, mvs);
 #pragma unroll
@@ -902,7 +941,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         for (int i = 0; i < 4; ++i) {
           const uint8_t *blk = vl + (4 * g + i) * VS + block_bytes(VT) * b;
           const uint8_t *vrow = blk + (VT == Q4_1 ? 4 : VT == Q5_0 ? 6 : 2);
-          u[i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
+          if constexpr (kHoistV) u[i] = ur[b][i];
+          else u[i] = VT == Q8_0 ? lds_u16(vrow + 2 * n) : lds_u8(vrow + n);
           if constexpr (VT == Q5_0) {
             // element n: low nibble + high bit n; element n + 16: high nibble +
             // high bit n + 16; as two 5-bit values in bytes 0 and 1
@@ -987,17 +1027,33 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       RD4_TP();
       const uint8_t *kl = ring + (i % R) * TB;
       vl = kl + KCH * 16;
+      // q8_0 K words of this lane's key row for the int8 QK product
+      uint32_t kw[kI8 ? 16 : 1], ke[kI8 ? 4 : 1];
       if constexpr (DT > 0) {  // f16 scales (and offsets) of the tile -> f32 tables, once per tile
+        // the raw f16 words are read first, so that the K words' batch below
+        // (which waits for every LDS read of the wave) lands them in the same
+        // round trip
+        uint16_t raw[DT / 256];
 #pragma unroll
         for (int j = 0; j < DT / 256; ++j) {
           const int v = lane + 64 * j;
           const int ti = v >> 7, key = v & 15, b = (v >> 4) & 7;
-          float d;
-          if (ti == iDK) d = scale_of<KT>(kl + key * KS, b);
-          else if (ti == iDV) d = scale_of<VT>(vl + key * VS, b);
-          else if (ti == iMK) d = offset_of<KT>(kl + key * KS, b);
-          else d = offset_of<VT>(vl + key * VS, b);
-          dk_t[v] = d;
+          const uint8_t *src = ti == iDK   ? kl + key * KS + block_bytes(KT) * b
+                               : ti == iDV ? vl + key * VS + block_bytes(VT) * b
+                               : ti == iMK ? kl + key * KS + block_bytes(KT) * b + 2
+                                           : vl + key * VS + block_bytes(VT) * b + 2;
+          raw[j] = (uint16_t)lds_u16(src);
+        }
+        if constexpr (kI8 && kSqReg) {
+          k_words_q8(kl + n * KS, g, kw, ke);
+#pragma unroll
+          for (int j = 0; j < DT / 256; ++j) dk_t[lane + 64 * j] = h2f(raw[j]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < DT / 256; ++j) {
+            dk_t[lane + 64 * j] = h2f(raw[j]);
+            __builtin_amdgcn_sched_barrier(0);  // convert each word as it lands
+          }
         }
         wave_sync();
       }
@@ -1011,15 +1067,30 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         const uint8_t *krow = kl + n * KS;
         if constexpr (kI8) {
           floatx4 dks[8];
-          uint32_t kw[16], ke[4];
-          k_words_q8(krow, g, kw, ke);
-          tbl_read8(dk_t + 4 * g, dks);
+          float sqv[8];
+          if constexpr (kSqReg) {
+            tbl_read8(dk_t + 4 * g, dks);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) sqv[b] = sqb[b];
+          } else {
+            // (with q4_1 V, whose tables hold more registers, the K words and the
+            // block scales are read here)
+            k_words_q8(krow, g, kw, ke);
+            floatx4 s0, s1;
+            tbl_read8_q2(dk_t + 4 * g, (const float *)(q_lds + kG * (kHD * 4 + 16) + 256 + 16 * kHD) + 8 * n,
+                         dks, s0, s1);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              sqv[b] = s0[b];
+              sqv[b + 4] = s1[b];
+            }
+          }
 #pragma unroll
           for (int b = 0; b < 8; ++b) {
             const i32x4 z = {0, 0, 0, 0};
             const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(k_op_i8(kw, ke, b, sel_edge), qop[b], z, 0, 0, 0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = fmaf(dks[b][e], (float)c[e] * sqb[b], acc[e]);
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(dks[b][e], (float)c[e] * sqv[b], acc[e]);
           }
         } else if constexpr (KT == F16) {
 #pragma unroll
