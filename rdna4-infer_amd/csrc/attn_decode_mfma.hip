@@ -456,6 +456,21 @@ __device__ __forceinline__ void tbl_read8(const float *p, floatx4 (&out)[8]) {
       : "v"(a)
       : "memory");
 }
+// x[i] of lane n ^ 8 within each 16-lane row (row_ror:8), for the four
+// elements, as DPP moves in asm: the compiler does not fold them into the
+// following adds (its DPP combine of this exchange miscompiled). s_nop 1 covers
+// the VALU-write -> DPP-read hazard, which the compiler cannot see in asm.
+__device__ __forceinline__ floatx4 ror8x4(floatx4 x) {
+  floatx4 r;
+  __asm__("s_nop 1\n\t"
+          "v_mov_b32_dpp %0, %4 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+          "v_mov_b32_dpp %1, %5 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+          "v_mov_b32_dpp %2, %6 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+          "v_mov_b32_dpp %3, %7 row_ror:8 row_mask:0xf bank_mask:0xf"
+          : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+          : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
+  return r;
+}
 // tbl_read8 plus the two float4 at q (8 consecutive floats), in one batch.
 __device__ __forceinline__ void tbl_read8_q2(const float *p, const float *q, floatx4 (&out)[8], floatx4 &q0,
                                              floatx4 &q1) {
@@ -1127,13 +1142,24 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       // last key this lane's row may see, relative to the tile: pair mode masks the
       // second token's last key in the first token's rows
       const int lim = pair ? min(nk - 1, row_last - j_tile) : nk - 1;
+      // hi + lo rows: lane n ^ 8 by a DPP rotate (no LDS round trip) for q8_0 and
+      // f16 K; the nibble types keep the lane shuffle, which measured faster there
+      floatx4 acc8 = acc;
+      if constexpr (!PAIR) {
+        if constexpr (KT == Q8_0 || KT == F16) {
+          acc8 = ror8x4(acc);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc8[i] = xor_f(acc[i], 8);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v;
         if constexpr (kI8) {
-          v = acc[i] + xor_f(acc[i], 8);
+          v = acc[i] + acc8[i];
         } else {
-          v = pair ? acc[i] * sl2 : (acc[i] + xor_f(acc[i], 8)) * sl2;
+          v = pair ? acc[i] * sl2 : (acc[i] + acc8[i]) * sl2;
         }
         if (4 * g + i > lim) v = -INFINITY;
         sc[i] = v;
