@@ -177,13 +177,6 @@ __host__ __device__ constexpr int k_dim(int b, int g, int j) {
   return 32 * b + (j < 4 ? 26 + j : j == 4 ? 0 : j == 5 ? 1 : j == 6 ? 30 : 31);
 }
 
-// k-slot (g, j) of dim e (0..31) of block b under k_dim<Q8_0>: the inverse map,
-// used to lay the int8 query rows out in fragment order.
-__device__ __forceinline__ int q8_slot(int b, int e) {
-  if (b & 1) return e;  // g = e / 8, j = e % 8
-  if (e >= 2 && e < 26) return e - 2;
-  return e < 2 ? 28 + e : (e < 30 ? 24 + (e - 26) : 30 + (e - 30));
-}
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 // Max of a non-negative float over each group of 8 lanes (8k .. 8k + 7), in
@@ -762,6 +755,14 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       }
     }
   } else if constexpr (kI8) {
+    if (RD4_DEC_KNOBS && (a.dbg & 64)) {  // profiling knob: skip the query preparation
+#pragma unroll
+      for (int b = 0; b < 8; ++b) qop[b] = 0;
+      if constexpr (kSqReg) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b) sqb[b] = 0.0f;
+      }
+    } else {
     // wave w quantizes head rows w, w + kWaves, ...: lane l holds dims 4l..4l+3
     // of block l / 8; per block s_hi = amax / 127, q_hi = rint(q / s_hi), and the
     // remainder on s_hi / 254. The int8 image lies past the query rows, so no
@@ -788,20 +789,39 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       }
       if (r >= G) xr[0] = xr[1] = xr[2] = xr[3] = 0.0f;
       const float am = max8_nonneg(fmaxf(fmaxf(fabsf(xr[0]), fabsf(xr[1])), fmaxf(fabsf(xr[2]), fabsf(xr[3]))));
-      const float s_hi = am / 127.0f, s_lo = s_hi / 254.0f;
-      const float i_hi = am > 0.0f ? 127.0f / am : 0.0f, i_lo = am > 0.0f ? 254.0f * 127.0f / am : 0.0f;
+      // any scales work as long as the reconstruction uses the same ones: s_hi =
+      // amax / 127 and s_lo = s_hi / 254 by multiplication, the inverses from one
+      // v_rcp_f32 (a q_hi off by one from rounding is absorbed by the lo part)
+      const float rcp = am > 0.0f ? __builtin_amdgcn_rcpf(am) : 0.0f;
+      const float s_hi = am * (1.0f / 127.0f), s_lo = am * (1.0f / (127.0f * 254.0f));
+      const float i_hi = 127.0f * rcp, i_lo = (127.0f * 254.0f) * rcp;
+      uint32_t bh[4], bl[4];  // the int8 hi / lo values as bytes
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float qh = fminf(fmaxf(rintf(xr[i] * i_hi), -127.0f), 127.0f);
+        const float qh = __builtin_amdgcn_fmed3f(rintf(xr[i] * i_hi), -127.0f, 127.0f);
         const float rem = fmaf(-s_hi, qh, xr[i]);
-        const float ql = fminf(fmaxf(rintf(rem * i_lo), -127.0f), 127.0f);
-        const int d = 4 * lane + i, b = d >> 5, slot = q8_slot(b, d & 31);
-        qi[(r * 8 + b) * 32 + slot] = (uint8_t)(int8_t)qh;
-        qi[((r + 8) * 8 + b) * 32 + slot] = (uint8_t)(int8_t)ql;
+        const float ql = __builtin_amdgcn_fmed3f(rintf(rem * i_lo), -127.0f, 127.0f);
+        bh[i] = (uint32_t)(int)qh & 0xffu;
+        bl[i] = (uint32_t)(int)ql & 0xffu;
+      }
+      // lane l holds dims e = 4(l & 7) + i of block b = l / 8. Their k-slots (the
+      // inverse of k_dim<Q8_0>): odd blocks e (one aligned word); even blocks
+      // e - 2 for 2 <= e < 30, 28 + e below, e above (two aligned 16-bit pairs)
+      const int b = lane >> 3, e0 = 4 * (lane & 7);
+      uint8_t *hrow = qi + (r * 8 + b) * 32, *lrow = qi + ((r + 8) * 8 + b) * 32;
+      if (b & 1) {
+        *(uint32_t *)(hrow + e0) = bh[0] | bh[1] << 8 | bh[2] << 16 | bh[3] << 24;
+        *(uint32_t *)(lrow + e0) = bl[0] | bl[1] << 8 | bl[2] << 16 | bl[3] << 24;
+      } else {
+        const int s01 = e0 == 0 ? 28 : e0 - 2, s23 = e0 == 28 ? 30 : e0;
+        *(uint16_t *)(hrow + s01) = (uint16_t)(bh[0] | bh[1] << 8);
+        *(uint16_t *)(hrow + s23) = (uint16_t)(bh[2] | bh[3] << 8);
+        *(uint16_t *)(lrow + s01) = (uint16_t)(bl[0] | bl[1] << 8);
+        *(uint16_t *)(lrow + s23) = (uint16_t)(bl[2] | bl[3] << 8);
       }
       if ((lane & 7) == 0) {
-        sq[r * 8 + (lane >> 3)] = s_hi * a.scale * kLog2e;
-        sq[(r + 8) * 8 + (lane >> 3)] = s_lo * a.scale * kLog2e;
+        sq[r * 8 + b] = s_hi * a.scale * kLog2e;
+        sq[(r + 8) * 8 + b] = s_lo * a.scale * kLog2e;
       }
     }
     __syncthreads();
@@ -809,6 +829,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     for (int b = 0; b < 8; ++b) {
       qop[b] = *(const long *)(qi + (n * 8 + b) * 32 + 8 * g);
       if constexpr (kSqReg) sqb[b] = sq[n * 8 + b];
+    }
     }
   } else {
     const int hh = n & 7;
