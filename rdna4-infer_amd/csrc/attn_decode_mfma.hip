@@ -588,7 +588,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         store_group4<KT>(x, u & 7, row, u >> 3);
     }
     // the new row reaches this CU's L1 before any wave loads it (workgroup
-    // scope; the barrier after the query staging orders it for the other waves)
+    // scope; a CTA barrier orders it for the other waves: the one after the query
+    // staging, or on the int8 query path the one after the query preparation, and
+    // this CTA issues no tile before it)
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   }
 
@@ -695,7 +697,24 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       }
     }
   };
-  if (!pair) issue_q();
+  // int8 query path: wave w stages the rows it quantizes itself (one load
+  // instruction per row), so it waits for its own rows only, with no barrier
+  auto issue_q_own = [&]() {
+    if (RD4_DEC_KNOBS && (a.dbg & 2048)) return;
+#pragma unroll
+    for (int m = 0; m < 8 / kWaves; ++m) {
+      const int r = w + kWaves * m;
+      if (r < G && lane < qcw) {
+        const uint8_t *src = (const uint8_t *)a.q +
+                             (((int64_t)tok * a.n_head + h0 + r) * kHD) * (a.q_f16 ? 2 : 4) + 16 * lane;
+        __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(q_lds + r * qsb), 16, 0, 0);
+      }
+    }
+  };
+  if (!pair) {
+    if constexpr (kI8) issue_q_own();
+    else issue_q();
+  }
 #ifndef RD4_DEC_PRE
 #define RD4_DEC_PRE 1
 #endif
@@ -716,7 +735,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     else if (after == 2) wait_vm<2 * NI>();
     else if (after == 1) wait_vm<NI>();
     else wait_vm<0>();
-    __syncthreads();
+    // every wave uses every row: the rows loaded by the other waves must land
+    // (the int8 path's barrier comes after its own preparation)
+    if constexpr (!kI8) __syncthreads();
   }
   RD4_TP();
 
