@@ -464,6 +464,18 @@ __device__ __forceinline__ floatx4 ror8x4(floatx4 x) {
           : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
   return r;
 }
+// x summed with its value in lane ^ 16, then in lane ^ 32 (all four lane groups),
+// by the gfx950 row and half-wave swaps: with x in both operands the two
+// registers come out holding x and its partner, in one order or the other. In
+// asm: through the builtins the compiler added one result to itself when both
+// inputs were the same value. s_nop 1 covers the VALU-write -> swap-read hazard.
+__device__ __forceinline__ float sum_groups4(float x) {
+  float a = x, b = x;
+  __asm__("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  float c = a + b, d = a + b;
+  __asm__("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
+  return c + d;
+}
 // tbl_read8 plus the two float4 at q (8 consecutive floats), in one batch.
 __device__ __forceinline__ void tbl_read8_q2(const float *p, const float *q, floatx4 (&out)[8], floatx4 &q0,
                                              floatx4 &q1) {
@@ -1225,8 +1237,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   RD4_TP();
   // ---- wave state: l summed over the 4 key groups; the hi (n < 8) and lo
   // (n >= 8) rows of O go to LDS as separate rows and are added by the reader
-  l_run += xor_f(l_run, 16);
-  l_run += xor_f(l_run, 32);
+  l_run = sum_groups4(l_run);
 
   // ---- merge the waves through LDS (reuses the tile buffers). Row slots are
   // the 16 MFMA rows: single-token mode uses rows 0-7 (heads) and adds the lo
@@ -1277,45 +1288,34 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   }
   __syncthreads();
   RD4_TP();
-  float *ms = wo + kWaves * 16 * kRowPad;  // [kR] m (ln units), [kR] L, [kWaves][kR] weights
-  const int nhalf = pair ? 2 : 1;
-  for (int half = 0; half < nhalf; ++half) {
-    if (tid < kWaves * kG) {
-      // thread (wave ww, head hh); the max and the weighted sum run over ww
-      // (lane bits 3..) with lane exchanges, no serial loop
-      const int hh = tid % kG, ww = tid / kG, r = hh + 8 * half;
-      const float mw = wm[ww * kR + r];
-      float mm = mw;
-#pragma unroll
-      for (int x = kG; x < kWaves * kG; x <<= 1) mm = fmaxf(mm, xor_f(mm, x));
-      const float wt = (mm == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - mm);
-      float L = wt * wm[kWaves * kR + ww * kR + r];
-#pragma unroll
-      for (int x = kG; x < kWaves * kG; x <<= 1) L += xor_f(L, x);
-      ms[2 * kR + ww * kR + r] = wt;
-      if (ww == 0) {
-        ms[r] = (mm == -INFINITY) ? -INFINITY : mm * 0.6931471805599453f;  // log2 -> ln units
-        ms[kR + r] = L;
-      }
-    }
-  }
-  __syncthreads();
+  float *ms = wo + kWaves * 16 * kRowPad;  // in-kernel merge tree's LDS (flag and tables) past this
 
-  // output rows: (token tr, head hh) in MFMA row r = hh + 8 tr
+  // output rows: (token tr, head hh) in MFMA row r = hh + 8 tr. Each thread
+  // weighs the 8 wave states of its row itself (one LDS round trip for their m
+  // and l, no lane exchanges and no further barrier).
   const int nrow = pair ? ntc * G : G;
   for (int i = tid; i < nrow * kHD / 4; i += kThreads) {
     const int ri = i / (kHD / 4), d = 4 * (i - ri * (kHD / 4));
     const int tr = pair ? ri / G : 0, hh = ri - tr * G, r = hh + 8 * tr;
-    floatx4 acc4 = {0.f, 0.f, 0.f, 0.f};
+    float mw[kWaves], lw[kWaves];
+    float mm = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < kWaves; ++ww) {
-      floatx4 ov = *(const floatx4 *)(wo + (ww * 16 + r) * kRowPad + d);
-      acc4 += ms[2 * kR + ww * kR + r] * ov;
+      mw[ww] = wm[ww * kR + r];
+      lw[ww] = wm[kWaves * kR + ww * kR + r];
+      mm = fmaxf(mm, mw[ww]);
+    }
+    floatx4 acc4 = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float wt = (mm == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw[ww] - mm);
+      L = fmaf(wt, lw[ww], L);
+      acc4 += wt * *(const floatx4 *)(wo + (ww * 16 + r) * kRowPad + d);
     }
     const int64_t hrow_r = (int64_t)(tok + tr) * a.n_head + h0 + hh;
     if (a.n_splits == 1) {
-      const float L = ms[kR + r];
-      const float inv = (ms[r] == -INFINITY) ? 0.0f : ((L > 0.0f) ? 1.0f / L : 0.0f);
+      const float inv = (mm == -INFINITY) ? 0.0f : ((L > 0.0f) ? 1.0f / L : 0.0f);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         float o1 = acc4[k] * inv;
@@ -1329,16 +1329,15 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       }
     } else {
       *(floatx4 *)(rec_acc(a, hrow_r, s) + d) = acc4;
+      if (d == 0) {
+        float *ml = rec_ml(a, hrow_r, s);
+        ml[0] = (mm == -INFINITY) ? -INFINITY : mm * 0.6931471805599453f;  // log2 -> ln units
+        ml[1] = L;
+      }
     }
   }
   RD4_TP();
   if (a.n_splits == 1) return;
-  if (tid < nrow) {
-    const int tr = pair ? tid / G : 0, hh = tid - tr * G, r = hh + 8 * tr;
-    float *ml = rec_ml(a, (int64_t)(tok + tr) * a.n_head + h0 + hh, s);
-    ml[0] = ms[r];
-    ml[1] = ms[kR + r];
-  }
   int *flag = (int *)(ms + 2 * kR + kWaves * kR);
   if (pair || a.ext_merge || (a.dbg & 1)) return;
   split_tail<kThreads>(a, tok, kvh, hc, h0, G, s, flag, (float *)(flag + 4),
