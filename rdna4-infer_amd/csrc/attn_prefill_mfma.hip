@@ -61,6 +61,18 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ _Float16 h16(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
+// Max of x over lanes l, l ^ 16, l ^ 32, l ^ 48 by the gfx950 row and half-wave
+// swaps (no LDS round trip): with x in both operands the two registers come out
+// holding x and its partner. Asm with tied operands (the builtins mishandle equal
+// operands); s_nop 1 covers the VALU-write -> swap-read hazard.
+__device__ __forceinline__ float max_groups4(float x) {
+  float a = x, b = x;
+  __asm__("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  float c = fmaxf(a, b), d = c;
+  __asm__("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
+  return fmaxf(c, d);
+}
+
 }  // namespace
 
 __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p) {
@@ -330,8 +342,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
           s[sl][kt][i] = v;
           tmax = fmaxf(tmax, v);
         }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      tmax = max_groups4(tmax);
       // The reference max only moves when the block max exceeds it by more than
       // 2^8 (p <= 256 stays exact enough in f16 and l, O are f32): most blocks
       // then skip the O rescale.
