@@ -16,6 +16,54 @@ namespace {
 
 constexpr int kQuarterDims = 64;
 
+// Lane exchanges without LDS round trips: DPP within 16-lane rows (xor 1, xor 2,
+// then the half-row and row mirrors, which pair the 4- and 8-lane groups), and
+// the gfx950 row / half-wave swaps for lanes ^ 16 and ^ 32 (asm with tied
+// operands; s_nop 1 covers the VALU-write -> swap-read hazard).
+__device__ __forceinline__ float dpp_f(float x, int ctrl_sel) {
+  const int v = __builtin_bit_cast(int, x);
+  int r;
+  switch (ctrl_sel) {  // the DPP control must be a constant
+    case 0: r = __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
+    case 1: r = __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false); break;   // quad_perm 2,3,0,1
+    case 2: r = __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+    default: r = __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false); break; // row_mirror
+  }
+  return __builtin_bit_cast(float, r);
+}
+__device__ __forceinline__ void swap16(float &a, float &b) {
+  __asm__("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(float &a, float &b) {
+  __asm__("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) x = fmaxf(x, dpp_f(x, c));
+  float a = x, b = x;
+  swap16(a, b);
+  float c = fmaxf(a, b), d = c;
+  swap32(c, d);
+  return fmaxf(c, d);
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) x += dpp_f(x, c);
+  float a = x, b = x;
+  swap16(a, b);
+  float c = a + b, d = c;
+  swap32(c, d);
+  return c + d;
+}
+// x summed over lanes l, l ^ 16, l ^ 32, l ^ 48
+__device__ __forceinline__ float sum_groups4(float x) {
+  float a = x, b = x;
+  swap16(a, b);
+  float c = a + b, d = c;
+  swap32(c, d);
+  return c + d;
+}
+
 __global__ __launch_bounds__(64) void merge_splits_kernel(AttnArgs a) {
   __shared__ float w_s[kMaxSplits];
   const int lane = threadIdx.x;
@@ -49,8 +97,7 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(AttnArgs a) {
   float mm = -INFINITY;
 #pragma unroll
   for (int i = 0; i < kMaxSplits / 64; ++i) mm = fmaxf(mm, mv[i]);
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) mm = fmaxf(mm, xor_f(mm, m));
+  mm = wave_max(mm);
   float L = 0.0f;
 #pragma unroll
   for (int i = 0; i < kMaxSplits / 64; ++i) {
@@ -59,8 +106,7 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(AttnArgs a) {
     if (s < S) w_s[s] = w;
     L += w * lv[i];
   }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) L += xor_f(L, m);
+  L = wave_sum(L);
   __syncthreads();
   float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int s0 = sub;; s0 += 4 * kBatch) {
@@ -80,13 +126,10 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(AttnArgs a) {
       v[b] = s < S ? *(const float4 *)(acc + (int64_t)s * hd) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-#pragma unroll
-  for (int m = 16; m < 64; m <<= 1) {
-    sum.x += xor_f(sum.x, m);
-    sum.y += xor_f(sum.y, m);
-    sum.z += xor_f(sum.z, m);
-    sum.w += xor_f(sum.w, m);
-  }
+  sum.x = sum_groups4(sum.x);
+  sum.y = sum_groups4(sum.y);
+  sum.z = sum_groups4(sum.z);
+  sum.w = sum_groups4(sum.w);
   if (sub != 0) return;
   const float inv = (mm == -INFINITY) ? 0.0f : ((L > 0.0f) ? 1.0f / L : 0.0f);
   float ov[4] = {sum.x * inv, sum.y * inv, sum.z * inv, sum.w * inv};
