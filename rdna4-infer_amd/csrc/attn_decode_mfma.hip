@@ -709,22 +709,32 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       }
     }
   };
-  // int8 query path: wave w stages the rows it quantizes itself (one load
-  // instruction per row), so it waits for its own rows only, with no barrier
-  auto issue_q_own = [&]() {
-    if (RD4_DEC_KNOBS && (a.dbg & 2048)) return;
+  // int8 query path: wave w loads the rows it quantizes straight into registers
+  // (lane l: dims 4l..4l+3), ahead of its tile loads, so it waits for its own
+  // rows only, with no barrier and no LDS traffic
+  float xq[kI8 ? 8 / kWaves : 1][4];
+  auto load_q_own = [&]() {
 #pragma unroll
     for (int m = 0; m < 8 / kWaves; ++m) {
       const int r = w + kWaves * m;
-      if (r < G && lane < qcw) {
-        const uint8_t *src = (const uint8_t *)a.q +
-                             (((int64_t)tok * a.n_head + h0 + r) * kHD) * (a.q_f16 ? 2 : 4) + 16 * lane;
-        __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(q_lds + r * qsb), 16, 0, 0);
+      const int64_t off = ((int64_t)tok * a.n_head + h0 + (r < G ? r : 0)) * kHD + 4 * lane;
+      if (a.q_f16) {
+        const uint2 hv = *(const uint2 *)((const uint16_t *)a.q + off);
+        xq[m][0] = h2f((uint16_t)hv.x);
+        xq[m][1] = h2f((uint16_t)(hv.x >> 16));
+        xq[m][2] = h2f((uint16_t)hv.y);
+        xq[m][3] = h2f((uint16_t)(hv.y >> 16));
+      } else {
+        const float4 fv = *(const float4 *)(a.q + off);
+        xq[m][0] = fv.x;
+        xq[m][1] = fv.y;
+        xq[m][2] = fv.z;
+        xq[m][3] = fv.w;
       }
     }
   };
   if (!pair) {
-    if constexpr (kI8) issue_q_own();
+    if constexpr (kI8) load_q_own();
     else issue_q();
   }
 #ifndef RD4_DEC_PRE
@@ -805,21 +815,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
 #pragma unroll
     for (int m = 0; m < 8 / kWaves; ++m) {
       const int r = w + kWaves * m;
-      const uint8_t *qrow = q_lds + (r < G ? r : 0) * qsb;
-      float xr[4];
-      if (a.q_f16) {
-        const uint2 hv = *(const uint2 *)(qrow + 8 * lane);
-        xr[0] = h2f((uint16_t)hv.x);
-        xr[1] = h2f((uint16_t)(hv.x >> 16));
-        xr[2] = h2f((uint16_t)hv.y);
-        xr[3] = h2f((uint16_t)(hv.y >> 16));
-      } else {
-        const float4 fv = *(const float4 *)(qrow + 16 * lane);
-        xr[0] = fv.x;
-        xr[1] = fv.y;
-        xr[2] = fv.z;
-        xr[3] = fv.w;
-      }
+      float xr[4] = {xq[m][0], xq[m][1], xq[m][2], xq[m][3]};
       if (r >= G) xr[0] = xr[1] = xr[2] = xr[3] = 0.0f;
       const float am = max8_nonneg(fmaxf(fmaxf(fabsf(xr[0]), fabsf(xr[1])), fmaxf(fabsf(xr[2]), fabsf(xr[3]))));
       // any scales work as long as the reconstruction uses the same ones: s_hi =
