@@ -449,6 +449,87 @@ __device__ __forceinline__ void tbl_read8(const float *p, floatx4 (&out)[8]) {
       : "v"(a)
       : "memory");
 }
+// q4_0 / q4_1 K: the quant word of each of the 8 blocks that lane group g
+// converts (bytes 4g..4g+3 of the block's nibbles, as k_frag reads them) and the
+// 8 query fragments from LDS, in one asm batch that waits for its own LDS reads
+// (see k_words_q8). q4_0 blocks are 18 bytes: odd blocks' words are aligned,
+// even blocks' straddle two words; q4_1 blocks (20 bytes) are all aligned.
+template <int KT>
+__device__ __forceinline__ void k_words_q4(const uint8_t *krow, int g, const uint8_t *qfl,
+                                           uint32_t (&xw)[8], u32x4 (&qf)[8]) {
+  const uint32_t kb = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)(krow + 4 * g);
+  const uint32_t qa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)qfl;
+  u32x2 r[6];
+  if constexpr (KT == Q4_0) {
+    // dword offsets from krow + 4g: even b: 4.5b, +1; odd b: 4.5b + 0.5
+    __asm__ volatile(
+        "ds_read2_b32 %0, %14 offset0:0 offset1:1\n\t"
+        "ds_read2_b32 %1, %14 offset0:9 offset1:10\n\t"
+        "ds_read2_b32 %2, %14 offset0:18 offset1:19\n\t"
+        "ds_read2_b32 %3, %14 offset0:27 offset1:28\n\t"
+        "ds_read2_b32 %4, %14 offset0:5 offset1:14\n\t"
+        "ds_read2_b32 %5, %14 offset0:23 offset1:32\n\t"
+        "ds_read_b128 %6, %15\n\t"
+        "ds_read_b128 %7, %15 offset:1024\n\t"
+        "ds_read_b128 %8, %15 offset:2048\n\t"
+        "ds_read_b128 %9, %15 offset:3072\n\t"
+        "ds_read_b128 %10, %15 offset:4096\n\t"
+        "ds_read_b128 %11, %15 offset:5120\n\t"
+        "ds_read_b128 %12, %15 offset:6144\n\t"
+        "ds_read_b128 %13, %15 offset:7168\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(qf[0]),
+          "=&v"(qf[1]), "=&v"(qf[2]), "=&v"(qf[3]), "=&v"(qf[4]), "=&v"(qf[5]), "=&v"(qf[6]), "=&v"(qf[7])
+        : "v"(kb), "v"(qa)
+        : "memory");
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xw[2 * m] = __builtin_amdgcn_alignbyte(r[m][1], r[m][0], 2);
+    xw[1] = r[4][0];
+    xw[3] = r[4][1];
+    xw[5] = r[5][0];
+    xw[7] = r[5][1];
+  } else {
+    static_assert(KT == Q4_1, "q4_1 here");
+    // dword offsets from krow + 4g: 5b + 1
+    __asm__ volatile(
+        "ds_read2_b32 %0, %12 offset0:1 offset1:6\n\t"
+        "ds_read2_b32 %1, %12 offset0:11 offset1:16\n\t"
+        "ds_read2_b32 %2, %12 offset0:21 offset1:26\n\t"
+        "ds_read2_b32 %3, %12 offset0:31 offset1:36\n\t"
+        "ds_read_b128 %4, %13\n\t"
+        "ds_read_b128 %5, %13 offset:1024\n\t"
+        "ds_read_b128 %6, %13 offset:2048\n\t"
+        "ds_read_b128 %7, %13 offset:3072\n\t"
+        "ds_read_b128 %8, %13 offset:4096\n\t"
+        "ds_read_b128 %9, %13 offset:5120\n\t"
+        "ds_read_b128 %10, %13 offset:6144\n\t"
+        "ds_read_b128 %11, %13 offset:7168\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(qf[0]), "=&v"(qf[1]), "=&v"(qf[2]),
+          "=&v"(qf[3]), "=&v"(qf[4]), "=&v"(qf[5]), "=&v"(qf[6]), "=&v"(qf[7])
+        : "v"(kb), "v"(qa)
+        : "memory");
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      xw[2 * m] = r[m][0];
+      xw[2 * m + 1] = r[m][1];
+    }
+  }
+}
+// A operand of S^T = K Q^T for a q4_0 / q4_1 block from its quant word x (as
+// k_frag builds it)
+template <int KT>
+__device__ __forceinline__ half8 k_frag_q4word(uint32_t x) {
+  constexpr int BIAS = KT == Q4_0 ? -8 : 0;
+  const uint32_t x8 = x >> 8;
+  u32x4 r;
+  r[0] = nib_lo_h2<BIAS>(x);
+  r[1] = nib_lo_h2<BIAS>(x8);
+  r[2] = nib_hi_h2<BIAS>(x);
+  r[3] = nib_hi_h2<BIAS>(x8);
+  return __builtin_bit_cast(half8, r);
+}
+
 // x[i] of lane n ^ 8 within each 16-lane row (row_ror:8), for the four
 // elements, as DPP moves in asm: the compiler does not fold them into the
 // following adds (its DPP combine of this exchange miscompiled). s_nop 1 covers
@@ -1094,6 +1175,10 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       vl = kl + KCH * 16;
       // q8_0 K words of this lane's key row for the int8 QK product
       uint32_t kw[kI8 ? 16 : 1], ke[kI8 ? 4 : 1];
+      // q4_0 / q4_1 K words and the query fragments, batched the same way
+      constexpr bool kQ4 = (KT == Q4_0 || KT == Q4_1) && !PAIR && RD4_DEC_QLDS;
+      uint32_t xw[kQ4 ? 8 : 1];
+      u32x4 qfr[kQ4 ? 8 : 1];
       if constexpr (DT > 0) {  // f16 scales (and offsets) of the tile -> f32 tables, once per tile
         // the raw f16 words are read first, so that the K words' batch below
         // (which waits for every LDS read of the wave) lands them in the same
@@ -1111,6 +1196,10 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         }
         if constexpr (kI8 && kSqReg) {
           k_words_q8(kl + n * KS, g, kw, ke);
+#pragma unroll
+          for (int j = 0; j < DT / 256; ++j) dk_t[lane + 64 * j] = h2f(raw[j]);
+        } else if constexpr (kQ4) {
+          k_words_q4<KT>(kl + n * KS, g, q_lds + 16 * lane, xw, qfr);
 #pragma unroll
           for (int j = 0; j < DT / 256; ++j) dk_t[lane + 64 * j] = h2f(raw[j]);
         } else {
@@ -1168,7 +1257,11 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
 #pragma unroll
           for (int b = 0; b < 8; ++b) {
             const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-            const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), q_frag(b), z, 0, 0, 0);
+            floatx4 c;
+            if constexpr (kQ4)
+              c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag_q4word<KT>(xw[b]), __builtin_bit_cast(half8, qfr[b]), z, 0, 0, 0);
+            else
+              c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), q_frag(b), z, 0, 0, 0);
             const float4 dk = make_float4(dks[b][0], dks[b][1], dks[b][2], dks[b][3]);
             acc[0] = fmaf(dk.x, c[0], acc[0]);
             acc[1] = fmaf(dk.y, c[1], acc[1]);
