@@ -516,6 +516,89 @@ __device__ __forceinline__ void k_words_q4(const uint8_t *krow, int g, const uin
     }
   }
 }
+// q5_0 K: for each of the 8 blocks the two realigned quant words that lane
+// group g converts (x, y as k_frag<Q5_0> reads them) and the block's 32 high
+// bits, plus the 8 query fragments from LDS, in one asm batch that waits for its
+// own LDS reads (see k_words_q8). Blocks are 22 bytes; a block pair spans 11
+// dwords, with the even block's words 2 bytes off alignment.
+__device__ __forceinline__ void k_words_q5(const uint8_t *krow, int g, const uint8_t *qfl, uint32_t (&x)[8],
+                                           uint32_t (&y)[8], uint32_t (&qh)[8], u32x4 (&qf)[8]) {
+  const uint32_t b1 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)(krow + 8 * (g & 1));
+  const uint32_t b0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)krow;
+  const uint32_t qa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)qfl;
+  u32x2 r1[10], r0[6];
+  __asm__ volatile(
+        "ds_read2_b32 %0, %24 offset0:1 offset1:2\n\t"
+        "ds_read2_b32 %1, %24 offset0:3 offset1:7\n\t"
+        "ds_read2_b32 %2, %24 offset0:8 offset1:12\n\t"
+        "ds_read2_b32 %3, %24 offset0:13 offset1:14\n\t"
+        "ds_read2_b32 %4, %24 offset0:18 offset1:19\n\t"
+        "ds_read2_b32 %5, %24 offset0:23 offset1:24\n\t"
+        "ds_read2_b32 %6, %24 offset0:25 offset1:29\n\t"
+        "ds_read2_b32 %7, %24 offset0:30 offset1:34\n\t"
+        "ds_read2_b32 %8, %24 offset0:35 offset1:36\n\t"
+        "ds_read2_b32 %9, %24 offset0:40 offset1:41\n\t"
+        "ds_read2_b32 %10, %25 offset0:0 offset1:1\n\t"
+        "ds_read2_b32 %11, %25 offset0:6 offset1:11\n\t"
+        "ds_read2_b32 %12, %25 offset0:12 offset1:17\n\t"
+        "ds_read2_b32 %13, %25 offset0:22 offset1:23\n\t"
+        "ds_read2_b32 %14, %25 offset0:28 offset1:33\n\t"
+        "ds_read2_b32 %15, %25 offset0:34 offset1:39\n\t"
+        "ds_read_b128 %16, %26\n\t"
+        "ds_read_b128 %17, %26 offset:1024\n\t"
+        "ds_read_b128 %18, %26 offset:2048\n\t"
+        "ds_read_b128 %19, %26 offset:3072\n\t"
+        "ds_read_b128 %20, %26 offset:4096\n\t"
+        "ds_read_b128 %21, %26 offset:5120\n\t"
+        "ds_read_b128 %22, %26 offset:6144\n\t"
+        "ds_read_b128 %23, %26 offset:7168\n\t"
+        "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r1[0]), "=&v"(r1[1]), "=&v"(r1[2]), "=&v"(r1[3]), "=&v"(r1[4]), "=&v"(r1[5]), "=&v"(r1[6]), "=&v"(r1[7]), "=&v"(r1[8]), "=&v"(r1[9]), "=&v"(r0[0]), "=&v"(r0[1]), "=&v"(r0[2]), "=&v"(r0[3]), "=&v"(r0[4]), "=&v"(r0[5]), "=&v"(qf[0]), "=&v"(qf[1]), "=&v"(qf[2]), "=&v"(qf[3]), "=&v"(qf[4]), "=&v"(qf[5]), "=&v"(qf[6]), "=&v"(qf[7])
+      : "v"(b1), "v"(b0), "v"(qa)
+      : "memory");
+    // blocks 0 (even) and 1 (odd)
+    qh[0] = __builtin_amdgcn_alignbyte(r0[0][1], r0[0][0], 2);
+    x[0] = __builtin_amdgcn_alignbyte(r1[0][1], r1[0][0], 2);
+    y[0] = __builtin_amdgcn_alignbyte(r1[1][0], r1[0][1], 2);
+    qh[1] = r0[1][0];
+    x[1] = r1[1][1];
+    y[1] = r1[2][0];
+    // blocks 2 (even) and 3 (odd)
+    qh[2] = __builtin_amdgcn_alignbyte(r0[2][0], r0[1][1], 2);
+    x[2] = __builtin_amdgcn_alignbyte(r1[3][0], r1[2][1], 2);
+    y[2] = __builtin_amdgcn_alignbyte(r1[3][1], r1[3][0], 2);
+    qh[3] = r0[2][1];
+    x[3] = r1[4][0];
+    y[3] = r1[4][1];
+    // blocks 4 (even) and 5 (odd)
+    qh[4] = __builtin_amdgcn_alignbyte(r0[3][1], r0[3][0], 2);
+    x[4] = __builtin_amdgcn_alignbyte(r1[5][1], r1[5][0], 2);
+    y[4] = __builtin_amdgcn_alignbyte(r1[6][0], r1[5][1], 2);
+    qh[5] = r0[4][0];
+    x[5] = r1[6][1];
+    y[5] = r1[7][0];
+    // blocks 6 (even) and 7 (odd)
+    qh[6] = __builtin_amdgcn_alignbyte(r0[5][0], r0[4][1], 2);
+    x[6] = __builtin_amdgcn_alignbyte(r1[8][0], r1[7][1], 2);
+    y[6] = __builtin_amdgcn_alignbyte(r1[8][1], r1[8][0], 2);
+    qh[7] = r0[5][1];
+    x[7] = r1[9][0];
+    y[7] = r1[9][1];
+}
+// A operand of S^T = K Q^T for a q5_0 block from its realigned words and high
+// bits (as k_frag<Q5_0> builds it)
+__device__ __forceinline__ half8 k_frag_q5words(uint32_t x, uint32_t y, uint32_t qh, int g) {
+  const int gg = g & 1, sh = (g & 2) ? 4 : 0;
+  x >>= sh;
+  y >>= sh;
+  const uint32_t hb = qh >> (16 * (g >> 1) + 8 * gg);
+  u32x4 r;
+  r[0] = q5pair_to_h2(x, 0x0c010c00u, hb & 1u, (hb >> 1) & 1u);
+  r[1] = q5pair_to_h2(x, 0x0c030c02u, (hb >> 2) & 1u, (hb >> 3) & 1u);
+  r[2] = q5pair_to_h2(y, 0x0c010c00u, (hb >> 4) & 1u, (hb >> 5) & 1u);
+  r[3] = q5pair_to_h2(y, 0x0c030c02u, (hb >> 6) & 1u, (hb >> 7) & 1u);
+  return __builtin_bit_cast(half8, r);
+}
 // A operand of S^T = K Q^T for a q4_0 / q4_1 block from its quant word x (as
 // k_frag builds it)
 template <int KT>
@@ -1177,8 +1260,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       uint32_t kw[kI8 ? 16 : 1], ke[kI8 ? 4 : 1];
       // q4_0 / q4_1 K words and the query fragments, batched the same way
       constexpr bool kQ4 = (KT == Q4_0 || KT == Q4_1) && !PAIR && RD4_DEC_QLDS;
-      uint32_t xw[kQ4 ? 8 : 1];
-      u32x4 qfr[kQ4 ? 8 : 1];
+      constexpr bool kQ5 = KT == Q5_0 && !PAIR && RD4_DEC_QLDS;
+      uint32_t xw[kQ4 || kQ5 ? 8 : 1], yw[kQ5 ? 8 : 1], hw[kQ5 ? 8 : 1];
+      u32x4 qfr[kQ4 || kQ5 ? 8 : 1];
       if constexpr (DT > 0) {  // f16 scales (and offsets) of the tile -> f32 tables, once per tile
         // the raw f16 words are read first, so that the K words' batch below
         // (which waits for every LDS read of the wave) lands them in the same
@@ -1198,8 +1282,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
           k_words_q8(kl + n * KS, g, kw, ke);
 #pragma unroll
           for (int j = 0; j < DT / 256; ++j) dk_t[lane + 64 * j] = h2f(raw[j]);
-        } else if constexpr (kQ4) {
-          k_words_q4<KT>(kl + n * KS, g, q_lds + 16 * lane, xw, qfr);
+        } else if constexpr (kQ4 || kQ5) {
+          if constexpr (kQ4) k_words_q4<KT>(kl + n * KS, g, q_lds + 16 * lane, xw, qfr);
+          else k_words_q5(kl + n * KS, g, q_lds + 16 * lane, xw, yw, hw, qfr);
 #pragma unroll
           for (int j = 0; j < DT / 256; ++j) dk_t[lane + 64 * j] = h2f(raw[j]);
         } else {
@@ -1260,6 +1345,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
             floatx4 c;
             if constexpr (kQ4)
               c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag_q4word<KT>(xw[b]), __builtin_bit_cast(half8, qfr[b]), z, 0, 0, 0);
+            else if constexpr (kQ5)
+              c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag_q5words(xw[b], yw[b], hw[b], g), __builtin_bit_cast(half8, qfr[b]), z, 0, 0, 0);
             else
               c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), q_frag(b), z, 0, 0, 0);
             const float4 dk = make_float4(dks[b][0], dks[b][1], dks[b][2], dks[b][3]);
