@@ -585,6 +585,36 @@ __device__ __forceinline__ void k_words_q5(const uint8_t *krow, int g, const uin
     x[7] = r1[9][0];
     y[7] = r1[9][1];
 }
+// f16 K: the lane's 8 K fragments (16-byte chunks of its key row at the
+// swizzled LDS addresses ka[b]) and the 8 query fragments from LDS, in one asm
+// batch that waits for its own LDS reads (see k_words_q8).
+__device__ __forceinline__ void k_words_f16(const uint32_t (&ka)[8], const uint8_t *qfl, u32x4 (&kf)[8],
+                                            u32x4 (&qf)[8]) {
+  const uint32_t qa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)qfl;
+  __asm__ volatile(
+      "ds_read_b128 %0, %16\n\t"
+      "ds_read_b128 %1, %17\n\t"
+      "ds_read_b128 %2, %18\n\t"
+      "ds_read_b128 %3, %19\n\t"
+      "ds_read_b128 %4, %20\n\t"
+      "ds_read_b128 %5, %21\n\t"
+      "ds_read_b128 %6, %22\n\t"
+      "ds_read_b128 %7, %23\n\t"
+      "ds_read_b128 %8, %24\n\t"
+      "ds_read_b128 %9, %24 offset:1024\n\t"
+      "ds_read_b128 %10, %24 offset:2048\n\t"
+      "ds_read_b128 %11, %24 offset:3072\n\t"
+      "ds_read_b128 %12, %24 offset:4096\n\t"
+      "ds_read_b128 %13, %24 offset:5120\n\t"
+      "ds_read_b128 %14, %24 offset:6144\n\t"
+      "ds_read_b128 %15, %24 offset:7168\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(kf[0]), "=&v"(kf[1]), "=&v"(kf[2]), "=&v"(kf[3]), "=&v"(kf[4]), "=&v"(kf[5]), "=&v"(kf[6]),
+        "=&v"(kf[7]), "=&v"(qf[0]), "=&v"(qf[1]), "=&v"(qf[2]), "=&v"(qf[3]), "=&v"(qf[4]), "=&v"(qf[5]),
+        "=&v"(qf[6]), "=&v"(qf[7])
+      : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(ka[4]), "v"(ka[5]), "v"(ka[6]), "v"(ka[7]), "v"(qa)
+      : "memory");
+}
 // A operand of S^T = K Q^T for a q5_0 block from its realigned words and high
 // bits (as k_frag<Q5_0> builds it)
 __device__ __forceinline__ half8 k_frag_q5words(uint32_t x, uint32_t y, uint32_t qh, int g) {
@@ -1085,6 +1115,12 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   // edge gather of the unaligned q8_0 K blocks: lane group 3 takes the block's
   // first and last byte pairs
   const uint32_t sel_edge = g == 3 ? 0x05040302u : 0x07060504u;
+  // f16 K: byte offset of block b's 16-byte chunk in the lane's swizzled key row
+  uint32_t kf16_off[KT == F16 ? 8 : 1];
+  if constexpr (KT == F16) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) kf16_off[b] = 16u * (uint32_t)((4 * b + g) ^ n);
+  }
   // pair mode: the last key of this lane's row; the P operand fills all 16 rows
   const int row_last = pair ? a.t + tok + (n >> 3) : t;
 
@@ -1332,9 +1368,21 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
             for (int e = 0; e < 4; ++e) acc[e] = fmaf(dks[b][e], (float)c[e] * sqv[b], acc[e]);
           }
         } else if constexpr (KT == F16) {
+          if constexpr (!PAIR && RD4_DEC_QLDS) {
+            uint32_t ka[8];
+            const uint32_t kr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)krow;
 #pragma unroll
-          for (int b = 0; b < 8; ++b)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), q_frag(b), acc, 0, 0, 0);
+            for (int b = 0; b < 8; ++b) ka[b] = kr + kf16_off[b];
+            u32x4 kfr[8], qfr8[8];
+            k_words_f16(ka, q_lds + 16 * lane, kfr, qfr8);
+#pragma unroll
+            for (int b = 0; b < 8; ++b)
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, kfr[b]), __builtin_bit_cast(half8, qfr8[b]), acc, 0, 0, 0);
+          } else {
+#pragma unroll
+            for (int b = 0; b < 8; ++b)
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag<KT>(krow, b, g, n, sel_edge), q_frag(b), acc, 0, 0, 0);
+          }
         } else {
           floatx4 dks[8], mks[KT == Q4_1 ? 8 : 1];
           tbl_read8(dk_t + 4 * g, dks);
