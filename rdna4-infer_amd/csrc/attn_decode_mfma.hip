@@ -643,6 +643,19 @@ __device__ __forceinline__ half8 k_frag_q4word(uint32_t x) {
   return __builtin_bit_cast(half8, r);
 }
 
+// A operand of the f16 product for a q8_0 block from the words k_words_q8 read
+// (as k_frag<Q8_0> builds it)
+__device__ __forceinline__ half8 k_frag_q8words(const uint32_t (&kw)[16], const uint32_t (&ke)[4], int b,
+                                                uint32_t sel_edge) {
+  const uint32_t x = kw[2 * b];
+  const uint32_t y = (b & 1) ? kw[2 * b + 1] : __builtin_amdgcn_perm(kw[2 * b + 1], ke[b >> 1], sel_edge);
+  u32x4 r;
+  r[0] = i8pair_to_h2(x, 0x0c010c00u);
+  r[1] = i8pair_to_h2(x, 0x0c030c02u);
+  r[2] = i8pair_to_h2(y, 0x0c010c00u);
+  r[3] = i8pair_to_h2(y, 0x0c030c02u);
+  return __builtin_bit_cast(half8, r);
+}
 // x[i] of lane n ^ 8 within each 16-lane row (row_ror:8), for the four
 // elements, as DPP moves in asm: the compiler does not fold them into the
 // following adds (its DPP combine of this exchange miscompiled). s_nop 1 covers
@@ -1293,7 +1306,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       const uint8_t *kl = ring + (i % R) * TB;
       vl = kl + KCH * 16;
       // q8_0 K words of this lane's key row for the int8 QK product
-      uint32_t kw[kI8 ? 16 : 1], ke[kI8 ? 4 : 1];
+      // (also for q8_0 K in pair mode, converted to f16 there)
+      constexpr bool kQ8W = kI8 || (KT == Q8_0 && PAIR);
+      uint32_t kw[kQ8W ? 16 : 1], ke[kQ8W ? 4 : 1];
       // q4_0 / q4_1 K words and the query fragments, batched the same way
       constexpr bool kQ4 = (KT == Q4_0 || KT == Q4_1) && !PAIR && RD4_DEC_QLDS;
       constexpr bool kQ5 = KT == Q5_0 && !PAIR && RD4_DEC_QLDS;
@@ -1314,7 +1329,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
                                            : vl + key * VS + block_bytes(VT) * b + 2;
           raw[j] = (uint16_t)lds_u16(src);
         }
-        if constexpr (kI8 && kSqReg) {
+        if constexpr ((kI8 && kSqReg) || (KT == Q8_0 && PAIR)) {
           k_words_q8(kl + n * KS, g, kw, ke);
 #pragma unroll
           for (int j = 0; j < DT / 256; ++j) dk_t[lane + 64 * j] = h2f(raw[j]);
@@ -1391,7 +1406,9 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
           for (int b = 0; b < 8; ++b) {
             const floatx4 z = {0.f, 0.f, 0.f, 0.f};
             floatx4 c;
-            if constexpr (kQ4)
+            if constexpr (KT == Q8_0 && PAIR)
+              c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag_q8words(kw, ke, b, sel_edge), q_frag(b), z, 0, 0, 0);
+            else if constexpr (kQ4)
               c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag_q4word<KT>(xw[b]), __builtin_bit_cast(half8, qfr[b]), z, 0, 0, 0);
             else if constexpr (kQ5)
               c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_frag_q5words(xw[b], yw[b], hw[b], g), __builtin_bit_cast(half8, qfr[b]), z, 0, 0, 0);
