@@ -302,6 +302,49 @@ print("ok")
         assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
 
 
+def test_in_kernel_merge_tree_env():
+    """RD4_DECODE_MERGE=2 selects the in-kernel counter-tree merge of the split
+    records instead of the merge launch (kept for comparison). Both must match
+    the oracle, over one merge level (16 splits) and two (64 splits), and repeat
+    bit for bit (the counters reset themselves). Child process: the library reads
+    the variable once."""
+    import subprocess
+    import sys
+    import os
+    code = r'''
+import sys
+sys.path.insert(0, "tests"); sys.path.insert(0, "oracle")
+import numpy as np, torch
+from conftest import load_package
+import oracle as orc
+from test_gpu_attn import make_cache
+from gpu_util import to_dev, check_close
+rd4 = load_package(); dev = torch.device("cuda:0")
+nh, nkv, hd, n = 24, 4, 256, 3000
+for kt, vt in ((2, 2), (3, 3), (1, 1)):
+    kh = make_cache(orc, kt, n, nkv, hd, 700 + kt, outlier=True)
+    vh = make_cache(orc, vt, n, nkv, hd, 710 + vt)
+    qh = orc.randn(nh * hd, 720)
+    want = orc.attn_decode(qh, kh, vh, n - 1, nh, nkv, hd, 1 / 16, kt, vt)
+    k, v, q = to_dev(kh, torch, dev), to_dev(vh, torch, dev), to_dev(qh, torch, dev)
+    for splits in (16, 64):
+        outs = []
+        for rep in range(2):
+            o = torch.empty(nh * hd, device=dev)
+            rd4.attn_decode(q, k, v, o, n - 1, nh, nkv, hd, 1 / 16, kt, vt, n_splits=splits)
+            torch.cuda.synchronize()
+            outs.append(o.cpu().numpy())
+        check_close(outs[0], want, "tree %d/%d splits %d" % (kt, vt, splits))
+        assert np.array_equal(outs[0], outs[1]), "repeat differs"
+print("ok")
+'''
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, RD4_DECODE_MERGE="2")
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True, text=True,
+                       timeout=180)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
 @pytest.mark.parametrize("kt", [1, 2])
 @pytest.mark.parametrize("shift", [20.0, -20.0])
 def test_merge_with_lse_spread(rd4, orc, dev, kt, shift):
