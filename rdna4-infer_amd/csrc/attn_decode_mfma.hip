@@ -945,13 +945,15 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     else issue_q();
   }
 #ifndef RD4_DEC_PRE
-#define RD4_DEC_PRE 1
+#define RD4_DEC_PRE 0
 #endif
-  // Tiles issued before the query rows have landed: one. The query rows gate
-  // the whole CTA, and more tile requests ahead of them (a chip-wide burst)
-  // delay them; the loop issues the rest of the ring at its start.
-  constexpr int kPre = RD4_DEC_PRE;
-  int next_issue = (RD4_DEC_PRE > 0 && !owns_new) ? min(kPre, my_tiles) : 0;  // next tile to issue
+  // Tiles issued before the query rows have landed: none. The query rows gate
+  // the whole CTA, and a chip-wide burst of tile requests queued with them at
+  // the memory controllers delays them (by about 2 us on q8_0 32K); the first
+  // tile goes out once they have landed, the rest of the ring at the loop start.
+  // (pair mode reads its query rows inside the preparation: one tile ahead)
+  constexpr int kPre = PAIR ? 1 : RD4_DEC_PRE;
+  int next_issue = (kPre > 0 && !owns_new) ? min(kPre, my_tiles) : 0;  // next tile to issue
   if (!owns_new) {
 #pragma unroll
     for (int i = 0; i < kPre; ++i)
@@ -969,6 +971,14 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     if constexpr (!kI8) __syncthreads();
   }
   RD4_TP();
+  // One tile requested as soon as the query rows are in, so it lands during the
+  // query preparation. (Two here, i.e. the whole ring, measured 2 us slower.)
+#ifndef RD4_DEC_POSTQ
+#define RD4_DEC_POSTQ 1
+#endif
+  if (RD4_DEC_POSTQ > 0 && !pair && !owns_new) {
+    while (next_issue < min(RD4_DEC_POSTQ, R) && next_issue < my_tiles) issue(next_issue++);
+  }
 
   // Query fragment (B operand of S^T = K Q^T): row n is head n (hi) or n-8
   // (lo); k-slot j of lane group g holds dim k_dim<KT>(b, g, j). Every wave
