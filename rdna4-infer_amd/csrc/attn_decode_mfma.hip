@@ -733,6 +733,48 @@ extern "C" int rd4_dec_trace_clear() {
 }
 #endif
 
+// CTA barrier for LDS data only: waits for this wave's LDS operations, not for
+// tile DMA still in flight (which __syncthreads would also wait for).
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The int8 query fragments (8 x 8 bytes, 32 bytes apart from p) and, when
+// wanted, the 8 row scales (from sq), in one batch of LDS reads with one wait
+// (plain loads would also wait for the tile DMA in flight).
+template <bool kScales>
+__device__ __forceinline__ void read_qop(const uint8_t *p, const float *sq, long (&qop)[8], float *sqb) {
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+  const uint32_t b = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)sq;
+#define RD4_QOP_READS                                                                                  \
+  "ds_read_b64 %0, %[a]\n\tds_read_b64 %1, %[a] offset:32\n\tds_read_b64 %2, %[a] offset:64\n\t"     \
+  "ds_read_b64 %3, %[a] offset:96\n\tds_read_b64 %4, %[a] offset:128\n\tds_read_b64 %5, %[a] offset:160\n\t" \
+  "ds_read_b64 %6, %[a] offset:192\n\tds_read_b64 %7, %[a] offset:224\n\t"
+  if constexpr (kScales) {
+    uint64_t s0, s1, s2, s3;  // scale pairs (64-bit outputs: a vector type here lost its upper halves)
+    __asm__ volatile(RD4_QOP_READS
+                     "ds_read_b64 %8, %[b]\n\tds_read_b64 %9, %[b] offset:8\n\t"
+                     "ds_read_b64 %10, %[b] offset:16\n\tds_read_b64 %11, %[b] offset:24\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(qop[0]), "=&v"(qop[1]), "=&v"(qop[2]), "=&v"(qop[3]), "=&v"(qop[4]), "=&v"(qop[5]),
+                       "=&v"(qop[6]), "=&v"(qop[7]), "=&v"(s0), "=&v"(s1), "=&v"(s2), "=&v"(s3)
+                     : [a] "v"(a), [b] "v"(b)
+                     : "memory");
+    const uint64_t sv[4] = {s0, s1, s2, s3};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sqb[2 * i] = __builtin_bit_cast(float, (uint32_t)sv[i]);
+      sqb[2 * i + 1] = __builtin_bit_cast(float, (uint32_t)(sv[i] >> 32));
+    }
+  } else {
+    (void)b;
+    (void)sqb;
+    __asm__ volatile(RD4_QOP_READS "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(qop[0]), "=&v"(qop[1]), "=&v"(qop[2]), "=&v"(qop[3]), "=&v"(qop[4]), "=&v"(qop[5]),
+                       "=&v"(qop[6]), "=&v"(qop[7])
+                     : [a] "v"(a)
+                     : "memory");
+  }
+#undef RD4_QOP_READS
+}
+
 template <int KT, int VT, bool PAIR>
 __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfma_kernel(AttnArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -971,14 +1013,21 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     if constexpr (!kI8) __syncthreads();
   }
   RD4_TP();
-  // One tile requested as soon as the query rows are in, so it lands during the
-  // query preparation. (Two here, i.e. the whole ring, measured 2 us slower.)
+  // One tile requested as soon as the query rows are in (on the LDS-staged query
+  // paths, once every wave has read them), so it lands during the query
+  // preparation. The preparation's barriers wait for LDS only: a CTA barrier
+  // would also wait for this tile.
 #ifndef RD4_DEC_POSTQ
 #define RD4_DEC_POSTQ 1
 #endif
-  if (RD4_DEC_POSTQ > 0 && !pair && !owns_new) {
-    while (next_issue < min(RD4_DEC_POSTQ, R) && next_issue < my_tiles) issue(next_issue++);
-  }
+  auto issue_postq = [&]() {
+    if (RD4_DEC_POSTQ > 0 && !pair && !owns_new) {
+      while (next_issue < min(RD4_DEC_POSTQ, R) && next_issue < my_tiles) issue(next_issue++);
+    }
+  };
+  // (f16 K measured faster with the tile requested here and landed by the
+  // preparation's CTA barriers)
+  if constexpr (kI8 || KT == F16) issue_postq();
 
   // Query fragment (B operand of S^T = K Q^T): row n is head n (hi) or n-8
   // (lo); k-slot j of lane group g holds dim k_dim<KT>(b, g, j). Every wave
@@ -1070,12 +1119,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         sq[(r + 8) * 8 + b] = s_lo * a.scale * kLog2e;
       }
     }
-    __syncthreads();
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      qop[b] = *(const long *)(qi + (n * 8 + b) * 32 + 8 * g);
-      if constexpr (kSqReg) sqb[b] = sq[n * 8 + b];
-    }
+    lds_barrier();
+    read_qop<kSqReg>(qi + n * 256 + 8 * g, sq + n * 8, qop, sqb);
     }
   } else {
     const int hh = n & 7;
@@ -1108,6 +1153,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       qsum_mine[m] = qs;
     }
     __syncthreads();  // every wave has read the query rows
+    if constexpr (KT != F16) issue_postq();
     u32x4 *qf_lds = (u32x4 *)q_lds;  // [block][lane]
     float *qsum_lds = (float *)(q_lds + 8 * 64 * 16);  // [block][head]
 #pragma unroll
@@ -1115,7 +1161,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       qf_lds[(w + kWaves * m) * 64 + lane] = mine[m];
       if (KT == Q4_1 && lane < 8) qsum_lds[(w + kWaves * m) * 8 + lane] = on ? qsum_mine[m] : 0.0f;
     }
-    __syncthreads();
+    if constexpr (KT == F16) __syncthreads();
+    else lds_barrier();
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
 #if !RD4_DEC_QLDS
