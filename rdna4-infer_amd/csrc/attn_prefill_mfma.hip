@@ -290,7 +290,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
     } else {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    __syncthreads();  // every wave's DMA for blk landed; every wave is done with blk - 1
+    // every wave's DMA for blk landed; every wave is done with blk - 1. A CTA
+    // barrier for LDS only: __syncthreads would also wait for K(blk + 1).
+#ifndef RD4_PF_FULLBAR
+    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#else
+    __syncthreads();
+#endif
     if (blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
     if (blk + 2 < n_blocks) issue_k(blk + 2, ks == 0 ? 2 : ks - 1);  // (blk + 2) % 3
     const uint8_t *kd = smem + ks * kKBytes;
