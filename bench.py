@@ -1,17 +1,25 @@
 """Benchmark of the full-attention hot path on one MI355X.
 
-Default workload (the metric's decode half): batch-1
-GQA decode, 24 q heads / 4 kv heads, head_dim 256, 32768 keys of q8_0 K/V
-(N(0,1) plus one x8 outlier dim per head), one step = append-and-quantize of
-the new token's K and V rows at position 32767 + gated split-KV attention over
-keys 0..32767. Inputs are resident in HBM before timing.
+Default run: both halves of the headline metric in one JSON line.
 
-value = algorithmic bytes of a step / step time (GB/s). The roofline object
-covers the dominant kernel (the attention launch), timed with HIP events on
-the stream the library launches on. cpu_baseline = the scalar CPU oracle (f64,
-one thread) on the same workload. `--workload prefill` measures BASELINE
-configs[4] instead (TFLOP/s of the causal QK^T + PV flops); `--extra` adds the
-other configs' numbers under "extra".
+- Decode: batch-1 GQA decode, 24 q heads / 4 kv
+  heads, head_dim 256, 32768 keys of q8_0 K/V (N(0,1) plus one x8 outlier dim
+  per head). One step is one token through the reference model's 16
+  full-attention layers: per layer, one rd4_attn_decode_append launch
+  (append-and-quantize of the token's K/V rows at position 32767 + gated
+  split-KV attention over keys 0..32767) on that layer's own cache. The 16
+  caches (1.14 GB) are larger than the 256 MB MALL, so every layer reads its
+  cache from HBM, as in a real decode step. The 16 launches are replayed as one
+  HIP graph (eager launches when --eager).
+- Prefill, under "prefill": 4096 f16 queries over 4096 + 4096
+  f16 keys, causal, gated, with the chunk's K/V rows appended as q8_0 in the
+  same rd4_prefill_append launch.
+
+value = algorithmic bytes of a step / step time (GB/s). Each roofline object
+covers that half's dominant kernel, timed with HIP events on the stream the
+library launches on. cpu_baseline = the scalar CPU oracle (f64, one thread) on
+a bounded sample of the same workload. `--workload X` measures one workload
+alone (for profiling); `--extra` adds the other configs under "extra".
 """
 import argparse
 import json
@@ -82,38 +90,49 @@ def event_loop_ms(torch, fn, steps):
     return a.elapsed_time(b) / steps
 
 
-def decode_workload(torch, rd4, kt, ctx, outlier, gated=True, vt=None):
-    """Returns (step_fn(timer), algorithmic step bytes, dominant-kernel bytes, cpu_fn, info)."""
+def decode_workload(torch, rd4, kt, ctx, outlier, gated=True, vt=None, layers=16):
+    """One decode token through `layers` attention layers, each with its own K/V
+    cache of `ctx` rows and its own q / gate / out / new rows.
+
+    Returns (step_fn, dominant_fn, step bytes, dominant bytes, cpu_fn, info);
+    the dominant kernel is the attention launch itself (one per layer), so
+    both are the same function here."""
     vt = kt if vt is None else vt
     pos = ctx - 1
     krb, vrb = rd4.kv_row_bytes(kt, HD), rd4.kv_row_bytes(vt, HD)
-    kc = make_cache(torch, rd4, kt, ctx, SEED, outlier)
-    vc = make_cache(torch, rd4, vt, ctx, SEED + 1, outlier)
     g = torch.Generator(device="cuda").manual_seed(SEED + 2)
-    q = torch.randn(NH * HD, generator=g, device="cuda")
-    gate0 = torch.randn(NH * HD, generator=g, device="cuda")
-    gate = gate0.clone()
-    krow = torch.randn(NKV * HD, generator=g, device="cuda")
-    vrow = torch.randn(NKV * HD, generator=g, device="cuda")
-    out = torch.empty(NH * HD, device="cuda")
+    L = []
+    for l in range(layers):
+        kc = make_cache(torch, rd4, kt, ctx, SEED + 10 * l, outlier)
+        vc = make_cache(torch, rd4, vt, ctx, SEED + 10 * l + 1, outlier)
+        q = torch.randn(NH * HD, generator=g, device="cuda")
+        gate = torch.randn(NH * HD, generator=g, device="cuda")
+        krow = torch.randn(NKV * HD, generator=g, device="cuda")
+        vrow = torch.randn(NKV * HD, generator=g, device="cuda")
+        out = torch.empty(NH * HD, device="cuda")
+        L.append((q, gate, krow, vrow, kc, vc, out))
     scale = 1.0 / np.sqrt(HD)
 
     def step():
-        # one launch: quantize-append the token's K/V rows at `pos`, gated attention over 0..pos
-        rd4.attn_decode_append(q, krow, vrow, kc, vc, out, pos, NH, NKV, HD, scale, kt, vt,
-                               gate=gate if gated else None)
+        # per layer, one launch: quantize-append the token's K/V rows at `pos`,
+        # then gated attention over keys 0..pos of that layer's cache
+        for (q, gate, krow, vrow, kc, vc, out) in L:
+            rd4.attn_decode_append(q, krow, vrow, kc, vc, out, pos, NH, NKV, HD, scale, kt, vt,
+                                   gate=gate if gated else None)
 
     kv_bytes = ctx * NKV * (krb + vrb)
     small = NH * HD * 4 * (4 if gated else 2)  # q, out (+ gate read and write)
     append = 2 * NKV * HD * 4 + NKV * (krb + vrb)
-    attn_bytes = kv_bytes + small + append  # the append is inside the attention launch
-    step_bytes = attn_bytes
+    layer_bytes = kv_bytes + small + append  # the append is inside the attention launch
+    step_bytes = layers * layer_bytes
 
     def cpu(budget_s=12.0, threads=1):
-        """f64 oracle on the same cache, repeated for ~budget_s; returns GB/s. threads > 1
-        runs its OpenMP form (parallel over heads)."""
+        """f64 oracle on layer 0's cache, repeated for ~budget_s; returns GB/s
+        (bytes of one layer over the time of one layer). threads > 1 runs its
+        OpenMP form (parallel over heads)."""
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as orc
+        q, gate, krow, vrow, kc, vc, out = L[0]
         kh, vh = kc.cpu().numpy(), vc.cpu().numpy()
         qh = q.cpu().numpy()
         reps, t0 = 0, time.perf_counter()
@@ -123,33 +142,38 @@ def decode_workload(torch, rd4, kt, ctx, outlier, gated=True, vt=None):
             if time.perf_counter() - t0 > budget_s:
                 break
         dt = (time.perf_counter() - t0) / reps
-        return attn_bytes / dt / 1e9, "full decode step over %d keys x %d reps" % (ctx, reps)
+        return layer_bytes / dt / 1e9, "one layer's decode over %d keys x %d reps" % (ctx, reps)
 
     kv_name = rd4.TYPE_NAMES[kt] if kt == vt else rd4.TYPE_NAMES[kt] + "/" + rd4.TYPE_NAMES[vt]
     info = {"workload": "decode", "kv_type": kv_name, "ctx": ctx, "n_head": NH,
-            "n_head_kv": NKV, "head_dim": HD, "gate": gated, "append": True, "seed": SEED}
-    return step, step, step_bytes, attn_bytes, cpu, info
+            "n_head_kv": NKV, "head_dim": HD, "gate": gated, "append": True, "seed": SEED,
+            "layers_per_step": layers, "kv_bytes_per_step": kv_bytes * layers}
+    return step, step, step_bytes, step_bytes, cpu, info
 
 
-def tokens_workload(torch, rd4, kt=2, ctx=32768, n_tok=4):
-    """MTP verify step: n_tok consecutive tokens ending at key ctx-1 attend (gated)
-    in one rd4_attn_decode_tokens launch; bytes = the K/V rows the tokens span
-    (read once would be ideal; each token reads them today)."""
+def tokens_workload(torch, rd4, kt=2, ctx=32768, n_tok=4, layers=16):
+    """MTP verify step: per layer, n_tok consecutive tokens ending at key ctx-1
+    attend (gated) in one rd4_attn_decode_tokens launch, each layer over its own
+    cache; bytes = the K/V rows the tokens span, read once."""
     krb = rd4.kv_row_bytes(kt, HD)
-    kc = make_cache(torch, rd4, kt, ctx, SEED, True)
-    vc = make_cache(torch, rd4, kt, ctx, SEED + 1, True)
     g = torch.Generator(device="cuda").manual_seed(SEED + 4)
-    q = torch.randn(n_tok * NH * HD, generator=g, device="cuda")
-    gate = torch.randn(n_tok * NH * HD, generator=g, device="cuda")
-    out = torch.empty_like(q)
+    L = []
+    for l in range(layers):
+        kc = make_cache(torch, rd4, kt, ctx, SEED + 10 * l, True)
+        vc = make_cache(torch, rd4, kt, ctx, SEED + 10 * l + 1, True)
+        q = torch.randn(n_tok * NH * HD, generator=g, device="cuda")
+        gate = torch.randn(n_tok * NH * HD, generator=g, device="cuda")
+        L.append((q, gate, kc, vc, torch.empty_like(q)))
 
     def step():
-        rd4.attn_decode_tokens(q, kc, vc, out, ctx - n_tok, n_tok, NH, NKV, HD, 1.0 / 16, kt, kt,
-                               gate=gate)
+        for (q, gate, kc, vc, out) in L:
+            rd4.attn_decode_tokens(q, kc, vc, out, ctx - n_tok, n_tok, NH, NKV, HD, 1.0 / 16, kt, kt,
+                                   gate=gate)
 
-    kv_bytes = ctx * NKV * 2 * krb + n_tok * NH * HD * 4 * 4
+    kv_bytes = layers * (ctx * NKV * 2 * krb + n_tok * NH * HD * 4 * 4)
     info = {"workload": "decode_tokens", "kv_type": rd4.TYPE_NAMES[kt], "ctx": ctx, "n_tok": n_tok,
-            "n_head": NH, "n_head_kv": NKV, "head_dim": HD, "gate": True, "seed": SEED}
+            "n_head": NH, "n_head_kv": NKV, "head_dim": HD, "gate": True, "seed": SEED,
+            "layers_per_step": layers}
     return step, step, kv_bytes, kv_bytes, None, info
 
 
@@ -204,6 +228,27 @@ def prefill_workload(torch, rd4, n_prefix=4096, n_q=4096):
     return step, attn, flops, flops, cpu, info
 
 
+def as_graph(torch, fn):
+    """fn's launches captured once into a HIP graph (torch.cuda.CUDAGraph);
+    returns its replay function, or None when capture is not possible."""
+    try:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        torch.cuda.synchronize()
+        return g.replay
+    except Exception as e:  # capture failed: measure eager launches instead
+        print("graph capture failed (%s); timing eager launches" % e, file=sys.stderr)
+        torch.cuda.synchronize()
+        return None
+
+
 def measure(torch, step, dominant, steps, warmup):
     """(ms per step, ms per dominant-kernel launch): the timed region is bracketed
     by synchronize() on both sides; the dominant kernel's own loop follows when
@@ -219,14 +264,73 @@ def measure(torch, step, dominant, steps, warmup):
     return max(wall_ms, ev_ms), dom_ms
 
 
+def decode_result(rd4, args, torch, name, graph=True):
+    """Measure one decode-style workload; returns (result fields, cpu_fn)."""
+    step, dom, step_units, dom_units, cpu, info = build_workload(torch, rd4, name, args)
+    runner = as_graph(torch, step) if graph else None
+    info["launch"] = "hip graph of the step's %d launches" % info["layers_per_step"] if runner else "eager"
+    run = runner or step
+    wall_ms, dom_ms = measure(torch, run, run, args.steps, args.warmup)
+    nl = info["layers_per_step"]
+    value = step_units / (wall_ms * 1e-3) / 1e9
+    achieved = dom_units / (dom_ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name),
+            "kernel_us": round(dom_ms * 1e3 / nl, 3),
+            "note": "per launch: one layer's attention (kernel_us), bytes of one layer / that time"}
+    info["us_per_token_layer"] = round(wall_ms * 1e3 / nl, 3)
+    return {"value": value, "wall_ms": wall_ms, "roofline": roof, "config": info}, cpu, step
+
+
+def prefill_result(rd4, args, torch):
+    step, dom, step_units, dom_units, cpu, info = build_workload(torch, rd4, "prefill", args)
+    steps = max(1, min(args.steps, 50))
+    wall_ms, dom_ms = measure(torch, step, dom, steps, min(args.warmup, 5))
+    value = step_units / (wall_ms * 1e-3) / 1e12
+    achieved = dom_units / (dom_ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": F16_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / F16_MFMA_PEAK_TFLOPS, 4),
+            "traffic": measured_traffic("prefill"), "kernel_ms": round(dom_ms, 4)}
+    return {"metric": "prefill attn TFLOP/s @4K causal", "value": round(value, 2), "unit": "TFLOP/s",
+            "ms_per_step": round(wall_ms, 5), "steps": steps,
+            "dtype": "f16 Q/K/V, f16 MFMA QK^T and PV, f32 accumulate and softmax",
+            "config": info, "roofline": roof}, cpu
+
+
+def build_workload(torch, rd4, name, args):
+    layers = args.layers
+    if name == "decode_q8_0":
+        return decode_workload(torch, rd4, 2, 32768, True, layers=layers)
+    if name == "decode_f16":
+        return decode_workload(torch, rd4, 1, 32768, False, layers=layers)
+    if name == "decode_q4_0":
+        return decode_workload(torch, rd4, 3, 131001, False, layers=max(1, layers // 4))
+    if name == "decode_q5_0_q4_1":  # the reference's 131K default pair
+        return decode_workload(torch, rd4, 4, 131001, False, vt=5, layers=max(1, layers // 4))
+    if name == "decode_tokens":  # MTP verify: 4 tokens at 32K, q8_0
+        return tokens_workload(torch, rd4, layers=layers)
+    return prefill_workload(torch, rd4)
+
+
+DTYPES = {
+    2: "q8_0 K/V: int8 MFMA QK^T (int8 hi/lo query parts), f16 MFMA PV (f16 p*d), f32 accumulate",
+    1: "f16 K/V: f16 MFMA QK^T (f16 hi/lo query parts) and PV, f32 accumulate",
+    3: "q4_0 K/V: f16 MFMA on exact f16 integers, per-block f32 scales, f32 accumulate",
+    4: "q5_0 K / q4_1 V: f16 MFMA on exact f16 integers, per-block f32 scales, f32 accumulate",
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="decode_q8_0",
-                    choices=["decode_q8_0", "decode_f16", "decode_q4_0", "decode_q5_0_q4_1",
+    ap.add_argument("--workload", default="headline",
+                    choices=["headline", "decode_q8_0", "decode_f16", "decode_q4_0", "decode_q5_0_q4_1",
                              "decode_tokens", "prefill", "copy"])
+    ap.add_argument("--layers", type=int, default=16,
+                    help="attention layers (each with its own cache) per decode step")
+    ap.add_argument("--eager", action="store_true", help="launch the decode step eagerly, no graph")
     ap.add_argument("--extra", action="store_true", help="also measure the other configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
@@ -250,77 +354,60 @@ def main():
                           "bytes_written": src.numel() * 4, "ms_per_copy": round(ms, 4)}))
         return
 
-    def build(name):
-        if name == "decode_q8_0":
-            return decode_workload(torch, rd4, 2, 32768, True)
-        if name == "decode_f16":
-            return decode_workload(torch, rd4, 1, 32768, False)
-        if name == "decode_q4_0":
-            return decode_workload(torch, rd4, 3, 131001, False)
-        if name == "decode_q5_0_q4_1":  # the reference's 131K default pair
-            return decode_workload(torch, rd4, 4, 131001, False, vt=5)
-        if name == "decode_tokens":  # MTP verify: 4 tokens at 32K, q8_0
-            return tokens_workload(torch, rd4)
-        return prefill_workload(torch, rd4)
-
-    step, dom, step_units, dom_units, cpu, info = build(args.workload)
-    wall_ms, dom_ms = measure(torch, step, dom, args.steps, args.warmup)
-    is_prefill = args.workload == "prefill"
-    if is_prefill:
-        metric, unit = "prefill attn TFLOP/s @4K causal", "TFLOP/s"
-        value = step_units / (wall_ms * 1e-3) / 1e12
-        achieved = dom_units / (dom_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": F16_MFMA_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / F16_MFMA_PEAK_TFLOPS, 4),
-                "traffic": measured_traffic(args.workload),
-                "kernel_ms": round(dom_ms, 4)}
-        dtype = "f16"
-    else:
-        metric, unit = "attn decode KV GB/s @32K ctx (q8_0 KV)", "GB/s"
-        if args.workload != "decode_q8_0":
-            metric = "attn decode KV GB/s (%s, %d keys)" % (info["kv_type"], info["ctx"])
-        value = step_units / (wall_ms * 1e-3) / 1e9
-        achieved = dom_units / (dom_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload),
-                "kernel_us": round(dom_ms * 1e3, 3)}
-        info["us_per_token_layer"] = round(wall_ms * 1e3, 3)
-        dtype = "f32"
-    res = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1,
-           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 5),
-           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
-           "data": "synthetic (seeded N(0,1), random K/V/Q/gate)", "config": info,
-           "roofline": roof}
-    if not args.no_cpu and cpu is not None:
+    def cpu_fields(cpu, unit, omp):
         v, sample = cpu()
-        res["cpu_baseline"] = {"value": round(v, 4), "unit": unit, "cores": 1, "kind": "port",
-                               "sample": sample + " (oracle/oracle.c, f64 accumulate)",
-                               "host_nproc": os.cpu_count()}
-        if not is_prefill:
+        out = {"cpu_baseline": {"value": round(v, 4), "unit": unit, "cores": 1, "kind": "port",
+                                "sample": sample + " (oracle/oracle.c, f64 accumulate)",
+                                "host_nproc": os.cpu_count()}}
+        if omp:
             # the optional multi-core form: OpenMP over heads, on the box's CPU share
             thr = max(1, min(16, os.cpu_count() or 1, NH))
             v2, sample2 = cpu(budget_s=5.0, threads=thr)
-            res["cpu_baseline_omp"] = {"value": round(v2, 4), "unit": unit, "cores": thr,
+            out["cpu_baseline_omp"] = {"value": round(v2, 4), "unit": unit, "cores": thr,
                                        "kind": "port", "sample": sample2}
+        return out
+
+    if args.workload == "prefill":
+        r, cpu = prefill_result(rd4, args, torch)
+        res = dict(r, n_gpus=1, warmup=args.warmup, higher_is_better=True, scaling="weak",
+                   vs_baseline=None, data="synthetic (seeded N(0,1), random K/V/Q/gate)")
+        if not args.no_cpu:
+            res.update(cpu_fields(cpu, "TFLOP/s", False))
+        print(json.dumps(res))
+        return
+
+    name = "decode_q8_0" if args.workload == "headline" else args.workload
+    r, cpu, _ = decode_result(rd4, args, torch, name, graph=not args.eager)
+    info = r["config"]
+    metric = "attn decode KV GB/s @32K ctx (q8_0 KV)"
+    if name != "decode_q8_0":
+        metric = "attn decode KV GB/s (%s, %d keys)" % (info["kv_type"], info["ctx"])
+    kt = {"decode_q8_0": 2, "decode_f16": 1, "decode_q4_0": 3, "decode_q5_0_q4_1": 4}.get(name, 2)
+    res = {"metric": metric, "value": round(r["value"], 3), "unit": "GB/s", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["wall_ms"], 5),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": DTYPES[kt],
+           "data": "synthetic (seeded N(0,1), random K/V/Q/gate)", "config": info,
+           "roofline": r["roofline"]}
+    if not args.no_cpu and cpu is not None:
+        res.update(cpu_fields(cpu, "GB/s", True))
+    if args.workload == "headline":
+        # the metric's second half: configs[4] prefill, measured in the same run
+        del cpu
+        torch.cuda.empty_cache()
+        p, pcpu = prefill_result(rd4, args, torch)
+        if not args.no_cpu:
+            p.update(cpu_fields(pcpu, "TFLOP/s", False))
+        res["prefill"] = p
     if args.extra:
         res["extra"] = {}
-        for name in ("decode_f16", "decode_q4_0", "decode_q5_0_q4_1", "decode_tokens", "prefill"):
-            if name == args.workload:
+        for w in ("decode_f16", "decode_q4_0", "decode_q5_0_q4_1", "decode_tokens"):
+            if w == name:
                 continue
-            st, dm, su, du, _, inf = build(name)
-            w, d = measure(torch, st, dm, 5 if name == "prefill" else 50, 3)
-            if name == "prefill":
-                res["extra"][name] = {"TFLOP/s": round(su / (w * 1e-3) / 1e12, 2),
-                                      "kernel_TFLOP/s": round(du / (d * 1e-3) / 1e12, 2),
-                                      "frac_of_mfma_peak": round(du / (d * 1e-3) / 1e12 / F16_MFMA_PEAK_TFLOPS, 4),
-                                      "ms_per_step": round(w, 4)}
-            else:
-                res["extra"][name] = {"GB/s": round(su / (w * 1e-3) / 1e9, 1),
-                                      "kernel_GB/s": round(du / (d * 1e-3) / 1e9, 1),
-                                      "frac_of_hbm_peak": round(du / (d * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                      "us_per_token_layer": round(w * 1e3, 2)}
-            del st
             torch.cuda.empty_cache()
+            e, _, _ = decode_result(rd4, argparse.Namespace(**dict(vars(args), steps=20, warmup=3)), torch, w)
+            res["extra"][w] = {"GB/s": round(e["value"], 1), "frac_of_hbm_peak": e["roofline"]["frac"],
+                               "us_per_token_layer": e["config"]["us_per_token_layer"],
+                               "layers_per_step": e["config"]["layers_per_step"]}
     print(json.dumps(res))
 
 

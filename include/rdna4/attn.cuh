@@ -2,10 +2,12 @@
 //
 // Same names and signatures as the reference (attn.cuh:56, 200, 373, 630, 665,
 // 895, 903, 958); every call forwards to librdna4attn's gfx950 kernels. The
-// `partial` buffers the caller passes are accepted and left untouched: the
-// library keeps split records in its own per-device scratch. n_splits is the
-// minimum split count the caller asks for (RD_ATTN_SPLITS keeps its meaning of
-// forcing a split path; the library may split further to fill the GPU).
+// `partial` buffer the caller passes receives the split records whenever the
+// split count the library runs fits it (attn_partial_bytes for the caller's
+// n_splits); otherwise the records go to the stream's own library scratch, so
+// launches on different streams never share records. n_splits is the minimum
+// split count the caller asks for (RD_ATTN_SPLITS keeps its meaning of forcing
+// a split path; the library may split further to fill the GPU).
 #pragma once
 #include <cstddef>
 
@@ -53,6 +55,17 @@ inline bool attn_launch_split_wpb(const float *d_q, const void *d_k, const void 
                                   int n_splits, int wpb, hipStream_t stream = nullptr) {
   return rd4_attn_launch_split_wpb(d_q, d_k, d_v, d_out, d_partial, t, n_head, n_head_kv,
                                    head_dim, scale, (int)kt, (int)vt, n_splits, wpb,
+                                   (void *)stream) == RD4_OK;
+}
+
+// Templated form of the bench overload (attn.cuh:613-628): the types are
+// template arguments, wpb is 8, 16 or 32.
+template <KvType KT, KvType VT>
+inline bool attn_launch_split_wpb(const float *d_q, const void *d_k, const void *d_v, float *d_out,
+                                  float *d_partial, int t, int n_head, int n_head_kv, int head_dim,
+                                  float scale, int n_splits, int wpb, hipStream_t stream) {
+  return rd4_attn_launch_split_wpb(d_q, d_k, d_v, d_out, d_partial, t, n_head, n_head_kv,
+                                   head_dim, scale, (int)KT, (int)VT, n_splits, wpb,
                                    (void *)stream) == RD4_OK;
 }
 

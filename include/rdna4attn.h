@@ -52,11 +52,17 @@ enum {
 
 /* Version string of this build. */
 const char *rd4_version(void);
-/* Create the per-device scratch (split-KV partials + merge counters) for the
- * current device. Called implicitly by the first attention launch on a device;
- * call it at init to keep allocation out of the first step. No counterpart in
- * the reference (its graph owned the partial buffer, graph.cuh:771-778). */
+/* Create the library scratch (split records + merge counters) of the null
+ * stream on the current device. Each stream gets its own scratch, so launches
+ * on different streams never share records or counters; a stream's scratch is
+ * created by its first split launch (hipMalloc plus a stream-ordered fill
+ * kernel, no synchronisation) unless rd4_init / rd4_stream_init made it
+ * first. Call them at init to keep allocation out of the first step. No
+ * counterpart in the reference (its graph owned the partial buffer,
+ * graph.cuh:771-778). */
 int rd4_init(void);
+/* The same for `stream` (a hipStream_t) on the current device. */
+int rd4_stream_init(void *stream);
 /* Human-readable reason of the last non-OK return on this thread. */
 const char *rd4_last_error(void);
 
@@ -109,9 +115,12 @@ int rd4_kv_load_rows_launch(int type, const void *src, float *dst, int64_t width
 /* attn_launch (attn.cuh:200): one query token [n_head][head_dim] f32. */
 int rd4_attn_launch(const float *q, const void *k, const void *v, float *out, int t, int n_head,
                     int n_head_kv, int head_dim, float scale, int kt, int vt, void *stream);
-/* attn_launch_split (attn.cuh:903). `partial` is accepted for source
- * compatibility and left untouched: the library keeps its partials in its own
- * scratch. n_splits >= 1 is the minimum key split count. */
+/* attn_launch_split (attn.cuh:903). n_splits >= 1 is the minimum key split
+ * count. `partial` (caller-owned, at least attn_partial_bytes(n_head,
+ * head_dim, n_splits) bytes, or NULL) receives the split records when the
+ * split count the library runs is at most n_splits, as in attn.cuh:593-608;
+ * otherwise the records go to the stream's library scratch. Either way, two
+ * streams never share records. A count the scratch cannot hold: RD4_EINVAL. */
 int rd4_attn_launch_split(const float *q, const void *k, const void *v, float *out,
                           float *partial, int t, int n_head, int n_head_kv, int head_dim,
                           float scale, int kt, int vt, int n_splits, void *stream);
@@ -165,8 +174,9 @@ int rd4_attn_decode_tokens(const float *q, const void *k, const void *v, float *
 int rd4_attn_batch_launch(const float *q, const void *k, const void *v, float *out,
                           const int *pos, int n_tok, int n_head, int n_head_kv, int head_dim,
                           float scale, int kt, int vt, void *stream);
-/* attn_split_batch_launch (attn.cuh:958): as above with n_splits key splits
- * per token; `partial` accepted and unused as in rd4_attn_launch_split. */
+/* attn_split_batch_launch (attn.cuh:958): as above with exactly n_splits key
+ * splits per token. `partial` (n_tok * attn_partial_bytes(n_head, head_dim,
+ * n_splits) bytes, or NULL) receives the records as in rd4_attn_launch_split. */
 int rd4_attn_split_batch_launch(const float *q, const void *k, const void *v, float *out,
                                 float *partial, const int *pos, int n_tok, int n_head,
                                 int n_head_kv, int head_dim, float scale, int kt, int vt,

@@ -24,6 +24,7 @@ SIGNATURES = {
     "rd4_kv_max_ctx": ([ctypes.c_uint64, ctypes.c_uint64] + [ctypes.c_int] * 5, ctypes.c_uint64),
     "rd4_version": ([], ctypes.c_char_p),
     "rd4_init": ([], _I),
+    "rd4_stream_init": ([_P], _I),
     "rd4_last_error": ([], ctypes.c_char_p),
     "rd4_kv_type_name": ([_I], ctypes.c_char_p),
     "rd4_kv_type_parse": ([ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)], ctypes.c_char_p),
@@ -189,8 +190,9 @@ def attn_batch(q, k, v, out, pos, n_head, n_head_kv, head_dim, scale, kt, vt):
            "attn_batch")
 
 
-def attn_split_batch(q, k, v, out, pos, n_head, n_head_kv, head_dim, scale, kt, vt, n_splits):
-    _check(lib().rd4_attn_split_batch_launch(_ptr(q), _ptr(k), _ptr(v), _ptr(out), None, _ptr(pos),
+def attn_split_batch(q, k, v, out, pos, n_head, n_head_kv, head_dim, scale, kt, vt, n_splits,
+                     partial=None):
+    _check(lib().rd4_attn_split_batch_launch(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(partial), _ptr(pos),
                                              pos.numel(), n_head, n_head_kv, head_dim, scale, kt,
                                              vt, n_splits, _stream()), "attn_split_batch")
 
@@ -259,3 +261,20 @@ def kv_cache_bytes(ctx_size, kt, vt, n_layers=None, n_head_kv=None, head_dim=Non
 def kv_max_ctx(budget_bytes, reserved_bytes, n_layers, n_head_kv, head_dim, kt, vt):
     """Largest context whose KV caches fit in budget_bytes - reserved_bytes."""
     return lib().rd4_kv_max_ctx(budget_bytes, reserved_bytes, n_layers, n_head_kv, head_dim, kt, vt)
+
+
+def init():
+    """rd4_init: create the null stream's library scratch on the current device."""
+    _check(lib().rd4_init(), "init")
+
+
+def stream_init(stream=None):
+    """rd4_stream_init: create the library scratch of `stream` (a torch stream,
+    default the current one) now instead of at its first split launch."""
+    import torch
+    st = stream if stream is not None else torch.cuda.current_stream()
+    _check(lib().rd4_stream_init(ctypes.c_void_p(st.cuda_stream)), "stream_init")
+
+
+def attn_partial_bytes(n_head, head_dim, n_splits):
+    return int(lib().rd4_attn_partial_bytes(n_head, head_dim, n_splits))

@@ -61,7 +61,8 @@ __global__ __launch_bounds__(kThreads) void attn_generic_kernel(AttnArgs a) {
   const int grp = a.n_head / a.n_head_kv;
   const int h0 = kvh * grp + hc * kGMax;            // first query head of this chunk
   const int G = min(kGMax, grp - hc * kGMax);      // heads in this chunk
-  const int t = a.pos ? a.pos[tok] : a.t + tok;  // consecutive positions without pos[]
+  int t = a.pos ? a.pos[tok] : a.t + tok;        // consecutive positions without pos[]
+  if (a.kcap > 0) t = min(t, a.kcap - 1);        // prefill: no key past kmax
   const int n_keys = t + 1;                        // may be <= 0: no keys
 
   // Contiguous key range of this split, in whole tiles.

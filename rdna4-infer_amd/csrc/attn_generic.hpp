@@ -18,6 +18,7 @@ struct AttnArgs {
   const float *v_new;     //   written to cache row t before it is attended
   const int *pos;         // device positions per token, or nullptr -> t
   int t;                  // last key index for the single-token launch
+  int kcap;               // > 0: keys from kcap on are never attended (prefill kmax + 1)
   int n_head, n_head_kv, head_dim;
   float scale;
   int n_splits;           // key splits per (token, kv head)

@@ -6,6 +6,8 @@
 // negative RD4_E* code in the same cases.
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <vector>
 #include <mutex>
 
 #include "../../include/rdna4attn.h"
@@ -17,6 +19,7 @@ hipError_t kv_store_launch(int t, const float *src, uint8_t *dst, int64_t width,
 hipError_t kv_fill_launch(int t, uint8_t *dst, int64_t n, uint32_t seed, hipStream_t st);
 hipError_t kv_load_launch(int t, const uint8_t *src, float *dst, int64_t n, hipStream_t st);
 hipError_t sigmoid_gate_launch(float *g, float *y, int64_t n, hipStream_t st);
+hipError_t fill_u32_launch(uint32_t *p, int64_t n, uint32_t v, hipStream_t st);
 hipError_t rope_launch(float *x, int n_tokens, int n_heads, int head_dim, int n_rot,
                        float freq_base, const int *pos, hipStream_t st);
 hipError_t rms_norm_launch(const float *x, const float *w, float *y, int64_t nrows, int64_t ncols,
@@ -47,39 +50,69 @@ int launched(hipError_t e, const char *what) {
 
 bool valid_type(int t) { return t >= 0 && t < kNumTypes; }
 
-// Per-device scratch: split partials (level 0 and level 1) and merge counters.
-// Sized once; a launch that would not fit uses fewer splits.
-constexpr int kMaxDevices = 64;
-constexpr int64_t kPartialFloats = 16ll << 20;  // 64 MiB
+// Library scratch for split records and merge counters, one set per (device,
+// stream): launches on different streams never share records or counters.
+// rd4_init creates the null stream's set and one spare. A stream seen for the
+// first time gets a new set made by hipMalloc plus a stream-ordered fill kernel
+// (no synchronisation), or, while it is capturing a HIP graph (when nothing may
+// be allocated), the spare. Sets are never freed. Caller-owned `partial` buffers are used instead when the
+// records fit (see run_attn).
+constexpr int64_t kPartialFloats = 16ll << 20;  // 64 MiB of records per stream
 constexpr int64_t kCounterWords = 1 << 20;
 struct Scratch {
   float *partial = nullptr;    // uncached: records exchanged between CTAs inside a launch
   float *partial_c = nullptr;  // cached: records handed to a later launch
   unsigned *counters = nullptr;
 };
-Scratch g_scratch[kMaxDevices];
+std::map<std::pair<int, uintptr_t>, Scratch> g_scratch;
+std::map<int, std::vector<Scratch>> g_spare;  // per device, made by rd4_init, not yet assigned
 std::mutex g_scratch_mu;
 
-int get_scratch(Scratch **out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(RD4_EINVAL, "no current HIP device%s");
+// A new set on the current device; its counters are zeroed on `st` (a fill
+// kernel), or at once with a blocking memset when `blocking`.
+int new_scratch(hipStream_t st, bool blocking, Scratch *out) {
+  Scratch n;
+  // Uncached: the generic kernel's split records cross XCDs inside one launch
+  // (see merge.hpp). Uncached memory is never freed once a kernel has read it.
+  if (hipExtMallocWithFlags((void **)&n.partial, kPartialFloats * sizeof(float),
+                            hipDeviceMallocUncached) != hipSuccess ||
+      hipMalloc(&n.partial_c, kPartialFloats * sizeof(float)) != hipSuccess ||
+      hipMalloc(&n.counters, kCounterWords * sizeof(unsigned)) != hipSuccess)
+    return fail(RD4_ENOMEM, "scratch allocation failed%s");
+  const bool ok = blocking ? hipMemset(n.counters, 0, kCounterWords * sizeof(unsigned)) == hipSuccess &&
+                                 hipDeviceSynchronize() == hipSuccess
+                           : fill_u32_launch(n.counters, kCounterWords, 0u, st) == hipSuccess;
+  if (!ok) return fail(RD4_ELAUNCH, "scratch counter fill failed%s");
+  *out = n;
+  return RD4_OK;
+}
+
+int current_device(int *dev) {
+  if (hipGetDevice(dev) != hipSuccess || *dev < 0) return fail(RD4_EINVAL, "no current HIP device%s");
+  return RD4_OK;
+}
+
+int get_scratch(hipStream_t st, Scratch **out) {
+  int dev = 0, rc;
+  if ((rc = current_device(&dev))) return rc;
   std::lock_guard<std::mutex> lk(g_scratch_mu);
-  Scratch &s = g_scratch[dev];
-  if (!s.partial) {
-    // Uncached: the split records cross XCDs inside one launch (see merge.hpp).
-    // Allocated once per device and never freed.
-    if (hipExtMallocWithFlags((void **)&s.partial, kPartialFloats * sizeof(float),
-                              hipDeviceMallocUncached) != hipSuccess)
-      return fail(RD4_ENOMEM, "scratch allocation failed%s");
-    if (hipMalloc(&s.partial_c, kPartialFloats * sizeof(float)) != hipSuccess ||
-        hipMalloc(&s.counters, kCounterWords * sizeof(unsigned)) != hipSuccess ||
-        hipMemset(s.counters, 0, kCounterWords * sizeof(unsigned)) != hipSuccess ||
-        hipDeviceSynchronize() != hipSuccess) {
-      return fail(RD4_ENOMEM, "counter allocation failed%s");
+  auto it = g_scratch.find({dev, (uintptr_t)st});
+  if (it == g_scratch.end()) {
+    Scratch n;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = st && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+    std::vector<Scratch> &sp = g_spare[dev];
+    if (!capturing) {
+      if ((rc = new_scratch(st, false, &n))) return rc;
+    } else if (!sp.empty()) {  // nothing may be allocated while a graph is captured
+      n = sp.back();
+      sp.pop_back();
+    } else {
+      return fail(RD4_ENOMEM, "no library scratch for this stream: call rd4_init or rd4_stream_init(stream) before capturing%s");
     }
+    it = g_scratch.emplace(std::make_pair(dev, (uintptr_t)st), n).first;
   }
-  *out = &s;
+  *out = &it->second;
   return RD4_OK;
 }
 
@@ -111,7 +144,8 @@ int auto_splits(int keys, int ctas_per_split, int target, int min_keys) {
 int run_attn(const float *q, const void *k, const void *v, float *out, float *gate,
              const int *pos, int t, int n_tok, int n_head, int n_head_kv, int head_dim,
              float scale, int kt, int vt, int splits, hipStream_t st,
-             const float *k_new = nullptr, const float *v_new = nullptr, int tok_pair = 0) {
+             const float *k_new = nullptr, const float *v_new = nullptr, int tok_pair = 0,
+             float *caller_partial = nullptr, int caller_splits = 0) {
   int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
   if (rc) return rc;
   if (n_tok < 1) return fail(RD4_EINVAL, "n_tok must be >= 1%s");
@@ -128,8 +162,9 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
     return e ? std::atoi(e) : 0;
   }();
   if (splits <= 0 && env_splits > 0) splits = env_splits > kMaxSplits ? kMaxSplits : env_splits;
+  const bool exact = splits > 0;
+  const int min_s = exact ? splits : -splits;
   if (splits <= 0) {  // automatic, at least -splits
-    const int min_s = -splits;
     // CTAs per split: every token's (kv head, head chunk) pairs; the keys of
     // the first token bound the split count
     // (token pairs share a CTA in the MFMA kernel's pair mode)
@@ -140,7 +175,10 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
     if (splits < min_s) splits = min_s;
   }
   if (splits < 1) splits = 1;
-  if (splits > kMaxSplits) splits = kMaxSplits;
+  if (splits > kMaxSplits) {
+    if (exact || min_s > kMaxSplits) return fail(RD4_EINVAL, "n_splits above the library's maximum (256)%s");
+    splits = kMaxSplits;
+  }
   AttnArgs a{};
   a.q = q;
   a.k = (const uint8_t *)k;
@@ -157,23 +195,52 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   a.scale = scale;
   a.tok_pair = tok_pair;
   if (splits > 1) {
-    Scratch *s = nullptr;
-    if ((rc = get_scratch(&s))) return rc;
-    // level-0 + level-1 records must fit; counters too.
-    auto floats_for = [&](int S) {
-      const int NG = (S + kMergeFan - 1) / kMergeFan;
-      return (int64_t)n_tok * n_head * (rec + 2) * (S + (NG > 1 ? NG : 0));
-    };
-    while (splits > 1 && floats_for(splits) > kPartialFloats) splits = (splits + 1) / 2;
-    const int64_t ctr_words = (int64_t)n_tok * n_head_kv * n_chunks * kCtrStride;
-    if (ctr_words > kCounterWords) splits = 1;
-    // The MFMA decode merges its records in a second launch (cached scratch
-    // suffices); the in-kernel merge tree needs the uncached one.
-    a.partial = (mfma && decode_mfma_ext_merge()) ? s->partial_c : s->partial;
-    a.counters = s->counters;
     const int64_t rows = (int64_t)n_tok * n_head;
+    const bool ext = mfma && decode_mfma_ext_merge();
+    const bool use_caller = ext && caller_partial && splits <= caller_splits;
+    if (!use_caller) {
+      // level-0 (+ level-1) records and the counters must fit the stream's scratch
+      auto fits = [&](int S, int64_t ntok) {
+        const int NG = (S + kMergeFan - 1) / kMergeFan;
+        return ntok * n_head * (rec + 2) * (S + (NG > 1 ? NG : 0)) <= kPartialFloats &&
+               ntok * n_head_kv * n_chunks * kCtrStride <= kCounterWords;
+      };
+      // an automatic count above the caller's minimum shrinks to fit first
+      while (!fits(splits, n_tok) && splits > min_s && splits > 1) --splits;
+      if (!fits(splits, n_tok)) {
+        if (!fits(splits, 1)) return fail(RD4_EINVAL, "split records of one token exceed the library scratch (64 MiB)%s");
+        // too many tokens at this split count: consecutive launches over token
+        // chunks, on the same stream (results are the same as one launch)
+        int per = 1;
+        while (fits(splits, 2 * per) && 2 * per < n_tok) per *= 2;
+        if (tok_pair && per > 1) per &= ~1;
+        for (int t0 = 0; t0 < n_tok; t0 += per) {
+          const int cnt = n_tok - t0 < per ? n_tok - t0 : per;
+          const int64_t off = (int64_t)t0 * n_head * head_dim;
+          rc = run_attn(q + off, k, v, out + off, gate ? gate + off : nullptr, pos ? pos + t0 : nullptr,
+                        pos ? t : t + t0, cnt, n_head, n_head_kv, head_dim, scale, kt, vt, splits, st,
+                        k_new, v_new, tok_pair, nullptr, 0);
+          if (rc) return rc;
+        }
+        return RD4_OK;
+      }
+    }
     const int NG = (splits + kMergeFan - 1) / kMergeFan;
     a.ml0_off = rows * splits * head_dim;
+    if (use_caller) {
+      // The caller's partial (sized attn_partial_bytes(n_head, hd, caller_splits)
+      // per token) holds the level-0 records [tok][head][split][hd] + (m, l), as
+      // in attn.cuh:593-608; the merge launch reads them on the same stream.
+      a.partial = caller_partial;
+      a.counters = nullptr;
+    } else {
+      Scratch *s = nullptr;
+      if ((rc = get_scratch(st, &s))) return rc;
+      // The MFMA decode merges its records in a second launch (cached scratch
+      // suffices); the in-kernel merge tree needs the uncached one.
+      a.partial = ext ? s->partial_c : s->partial;
+      a.counters = s->counters;
+    }
     a.acc1_off = a.ml0_off + rows * splits * 2;
     a.acc1_off = (a.acc1_off + 3) / 4 * 4;  // 16-byte aligned level-1 records
     a.ml1_off = a.acc1_off + rows * NG * head_dim;
@@ -193,8 +260,29 @@ extern "C" {
 const char *rd4_version(void) { return "rdna4attn-gfx950 0.1"; }
 
 int rd4_init(void) {
+  int dev = 0, rc;
+  if ((rc = current_device(&dev))) return rc;
+  // The null stream's set, and one spare for the next stream seen (a graph
+  // capture stream included), zeroed with a blocking memset: this is the init
+  // call, not a launch.
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch.count({dev, (uintptr_t)0})) {
+    Scratch n;
+    if ((rc = new_scratch(nullptr, true, &n))) return rc;
+    g_scratch.emplace(std::make_pair(dev, (uintptr_t)0), n);
+  }
+  std::vector<Scratch> &sp = g_spare[dev];
+  if (sp.empty()) {
+    Scratch n;
+    if ((rc = new_scratch(nullptr, true, &n))) return rc;
+    sp.push_back(n);
+  }
+  return RD4_OK;
+}
+
+int rd4_stream_init(void *stream) {
   Scratch *s = nullptr;
-  return get_scratch(&s);
+  return get_scratch((hipStream_t)stream, &s);
 }
 
 const char *rd4_last_error(void) { return g_err; }
@@ -331,12 +419,11 @@ int rd4_attn_launch(const float *q, const void *k, const void *v, float *out, in
 int rd4_attn_launch_split(const float *q, const void *k, const void *v, float *out,
                           float *partial, int t, int n_head, int n_head_kv, int head_dim,
                           float scale, int kt, int vt, int n_splits, void *stream) {
-  (void)partial;
   if (n_splits < 1) return fail(RD4_EINVAL, "n_splits must be >= 1%s");
   int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
   if (rc) return rc;
   return run_attn(q, k, v, out, nullptr, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt,
-                  vt, -n_splits, (hipStream_t)stream);
+                  vt, -n_splits, (hipStream_t)stream, nullptr, nullptr, 0, partial, n_splits);
 }
 
 int rd4_attn_launch_split_wpb(const float *q, const void *k, const void *v, float *out,
@@ -365,11 +452,10 @@ int rd4_attn_split_batch_launch(const float *q, const void *k, const void *v, fl
                                 float *partial, const int *pos, int n_tok, int n_head,
                                 int n_head_kv, int head_dim, float scale, int kt, int vt,
                                 int n_splits, void *stream) {
-  (void)partial;
   if (!pos) return fail(RD4_EINVAL, "pos must be a device array%s");
   if (n_splits < 1 || n_tok < 1) return fail(RD4_EINVAL, "n_splits and n_tok must be >= 1%s");
   return run_attn(q, k, v, out, nullptr, pos, 0, n_tok, n_head, n_head_kv, head_dim, scale, kt,
-                  vt, n_splits, (hipStream_t)stream);
+                  vt, n_splits, (hipStream_t)stream, nullptr, nullptr, 0, partial, n_splits);
 }
 
 int rd4_fa2_prefill_usable(int kt, int vt, int n_q, int pos0, int n_head, int n_head_kv,
@@ -451,6 +537,13 @@ int rd4_prefill_append(const void *q, int q_f16, const void *k, const void *v, f
   if (overlap(k_dst, app, k, att_k) || overlap(k_dst, app, v, att_v) || overlap(v_dst, app, k, att_k) ||
       overlap(v_dst, app, v, att_v) || overlap(k_dst, app, v_dst, app))
     return fail(RD4_EINVAL, "append destination overlaps the attended cache rows%s");
+  // The store launch's alignment rules hold on both paths (checked before
+  // anything is enqueued, so a refused call writes nothing).
+  const uintptr_t dst_al = dst_type == RD4_KV_F32 ? 15 : dst_type == RD4_KV_F16 ? 7 : 1;
+  if ((((uintptr_t)k_new) | (uintptr_t)v_new) & 15 || (((uintptr_t)k_dst) | (uintptr_t)v_dst) & dst_al)
+    return fail(RD4_EINVAL, "new rows must be 16-byte aligned, destinations aligned to their element store%s");
+  if (dst_type >= RD4_KV_Q8_0 && head_dim % 32 != 0)
+    return fail(RD4_EINVAL, "quantized append needs a head_dim that is a multiple of 32%s");
   const bool mfma = ((((uintptr_t)q) | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)gate |
                       (uintptr_t)k_new | (uintptr_t)v_new) & 15) == 0 &&
                     prefill_mfma_supported(kt, vt, n_head, n_head_kv, head_dim);

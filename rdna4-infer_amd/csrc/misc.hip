@@ -50,6 +50,21 @@ __global__ __launch_bounds__(128) void rope_kernel(float *__restrict__ x, int n_
   b[p + pairs] = rope_hi(x0, x1, c, s);
 }
 
+// Stream-ordered fill of library scratch words (a kernel, not hipMemsetAsync,
+// so a launch recorded into a HIP graph holds no memset node).
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t *__restrict__ p, int64_t n, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+hipError_t fill_u32_launch(uint32_t *p, int64_t n, uint32_t v, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, st, p,
+                     n, v);
+  return hipGetLastError();
+}
+
 hipError_t sigmoid_gate_launch(float *g, float *y, int64_t n, hipStream_t st) {
   if (n <= 0) return hipSuccess;
   const int64_t threads = (n + 3) / 4;

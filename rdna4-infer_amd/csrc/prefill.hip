@@ -30,6 +30,7 @@ hipError_t prefill_launch(int kt, int vt, const PrefillArgs &p, hipStream_t st) 
   a.gate = p.gate;
   a.pos = p.pos;
   a.t = p.pos0;
+  a.kcap = p.kmax + 1;  // keys 0..min(pos[i], kmax), as the reference's tiling bound
   a.n_head = p.n_head;
   a.n_head_kv = p.n_head_kv;
   a.head_dim = p.head_dim;

@@ -28,6 +28,11 @@ static_assert(std::is_same_v<decltype(&rms_norm_launch),
                              bool (*)(const float *, const float *, float *, std::int64_t,
                                       std::int64_t, float, hipStream_t)>);
 
+// The reference's templated bench overload (attn.cuh:613-628) keeps its form.
+static_assert(std::is_same_v<decltype(&attn_launch_split_wpb<KvType::Q8_0, KvType::Q8_0>),
+                             bool (*)(const float *, const void *, const void *, float *, float *,
+                                      int, int, int, int, float, int, int, hipStream_t)>);
+
 static int fails = 0;
 #define CHECK(c)                                              \
   do {                                                        \
@@ -37,7 +42,13 @@ static int fails = 0;
     }                                                         \
   } while (0)
 
-int main() {
+int main(int argc, char **argv) {
+  if (argc > 1 && std::strcmp(argv[1], "abort") == 0) {
+    // kv_unreachable (kv.h:58-69): a KvType outside the enum aborts the process
+    const auto n = kv_row_bytes((KvType)99, 256);
+    std::printf("no abort: %llu\n", (unsigned long long)n);
+    return 0;
+  }
   const KvType all[] = {KvType::F32, KvType::F16, KvType::Q8_0,
                         KvType::Q4_0, KvType::Q5_0, KvType::Q4_1};
   const unsigned long long rows[] = {1024, 512, 272, 144, 176, 160};
@@ -60,6 +71,10 @@ int main() {
                            KvType::F16, KvType::F16, 1));
   CHECK(!attn_launch_split_wpb(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 24, 4, 256, 1.f,
                                KvType::F16, KvType::F16, 1, 12));
+  {
+    auto typed = &attn_launch_split_wpb<KvType::F16, KvType::F16>;
+    CHECK(!typed(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 24, 4, 256, 1.f, 1, 12, nullptr));
+  }
   // device.h budget helpers (check_kvtype.hip:150-152 values)
   CHECK(kv_cache_bytes(131072, KvType::F16, KvType::F16) == 8589934592ull);
   CHECK(kv_cache_bytes(131072, "q8_0", "q8_0") == 4563402752ull);

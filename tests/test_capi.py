@@ -87,3 +87,20 @@ def test_fa2_usable_admission(rd4, monkeypatch):
     assert L.rd4_fa2_prefill_usable(2, 2, 512, 2048, 24, 4, 256) == 0  # f16/f16 only
     monkeypatch.setenv("RD_GFX12_FA2_PREFILL", "0")
     assert L.rd4_fa2_prefill_usable(1, 1, 512, 2048, 24, 4, 256) == 0
+
+
+def test_split_count_beyond_scratch_is_refused(rd4):
+    """A requested split count whose records do not fit the library scratch is an
+    error (RD4_EINVAL), not a silently smaller split; nothing is launched, so this
+    runs without a GPU. Neither is a count above the kernels' maximum (256)."""
+    L = rd4.lib()
+    fake = ctypes.c_void_p(0x10000)
+    # 256 heads x 256 splits: one token's records alone exceed the 64 MiB
+    # scratch (more tokens than fit are run as consecutive token chunks instead)
+    rc = L.rd4_attn_split_batch_launch(fake, fake, fake, fake, None, fake, 4, 256, 4, 256,
+                                       ctypes.c_float(1 / 16), 2, 2, 256, None)
+    assert rc == rd4.EINVAL
+    assert b"exceed the library scratch" in L.rd4_last_error()
+    rc = L.rd4_attn_launch_split(fake, fake, fake, fake, None, 100, 24, 4, 256, ctypes.c_float(1 / 16),
+                                 2, 2, 300, None)
+    assert rc == rd4.EINVAL and b"maximum" in L.rd4_last_error()

@@ -160,3 +160,57 @@ def test_prefill_append_rejects_overlap(rd4, orc, dev):
     with pytest.raises(rd4.Rd4Error):
         rd4.prefill_append(q, k, v, out, pos0, nh, nkv, hd, 1 / 16, 1, 1, src, src,
                            k[pos0 * nkv * rb:], v[pos0 * nkv * rb:], 1)
+
+
+def test_prefill_append_config5_full(rd4, orc, dev, monkeypatch):
+    """The launch bench.py times for configs[4] (rd4_prefill_append: 4096 f16
+    queries at 4096..8191 over 8192 f16 keys, causal, gated, the chunk's K/V rows
+    appended as q8_0), at full size (graph.cuh:1462 store + 1479-1535):
+    - all 4096 x 24 output rows against the generic (VALU) kernel on the same inputs;
+    - the first and last query row of every eighth 128-row CTA block, plus the
+      chunk's first and last rows, against the f64 oracle;
+    - the 4096 appended q8_0 rows of each cache byte-for-byte against the oracle's
+      quantization of the same f32 rows."""
+    import torch
+    nh, nkv, hd, pos0, nq = 24, 4, 256, 4096, 4096
+    n = pos0 + nq
+    k = orc.store_rows(1, orc.randn(n * nkv * hd, 81))
+    v = orc.store_rows(1, orc.randn(n * nkv * hd, 82))
+    q = orc.randn(nq * nh * hd, 83).reshape(nq, nh, hd).astype(np.float16)
+    g = orc.randn(nq * nh * hd, 84).reshape(nq, nh, hd)
+    knew = orc.randn(nq * nkv * hd, 85)
+    vnew = orc.randn(nq * nkv * hd, 86)
+    knew.reshape(nq, nkv, hd)[:, :, 7] *= 8  # the outlier channel of configs[2]
+    rb = rd4.kv_row_bytes(2, hd)
+    kq8 = torch.zeros(n * nkv * rb, dtype=torch.uint8, device=dev)
+    vq8 = torch.zeros_like(kq8)
+    qd, kd, vd = to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev)
+    out = torch.empty((nq, nh, hd), dtype=torch.float32, device=dev)
+    gd = to_dev(g, torch, dev)
+    off = pos0 * nkv * rb
+    rd4.prefill_append(qd, kd, vd, out, pos0, nh, nkv, hd, 1 / 16, 1, 1, to_dev(knew, torch, dev),
+                       to_dev(vnew, torch, dev), kq8[off:], vq8[off:], 2, gate=gd)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    sig = gd.cpu().numpy()
+    assert np.array_equal(kq8[off:].cpu().numpy(), orc.store_rows(2, knew))
+    assert np.array_equal(vq8[off:].cpu().numpy(), orc.store_rows(2, vnew))
+    assert not kq8[:off].any() and not vq8[:off].any()
+    # every row against the generic kernel
+    monkeypatch.setenv("RD4_PREFILL_GENERIC", "1")
+    ref = torch.empty_like(out)
+    gd2 = to_dev(g, torch, dev)
+    rd4.prefill(qd, kd, vd, ref, pos0, nh, nkv, hd, 1 / 16, 1, 1, gate=gd2)
+    torch.cuda.synchronize()
+    check_close(got.ravel(), ref.cpu().numpy().ravel(), "config 5 mfma vs generic, all rows")
+    assert np.array_equal(sig, gd2.cpu().numpy())
+    # CTA-boundary rows against the oracle: a CTA holds 128 (query, head) rows
+    grp = nh // nkv
+    blocks = range(0, (nq * grp + 127) // 128, 8)
+    rows = sorted({0, nq - 1} | {min(nq - 1, 128 * c // grp) for c in blocks} |
+                  {min(nq - 1, (128 * c + 127) // grp) for c in blocks})
+    rows = np.int32(rows)
+    want = orc.attn_batch(q[rows].astype(np.float32), k, v, pos0 + rows, nh, nkv, hd, 1 / 16, 1, 1,
+                          threads=8)
+    _, want = orc.sigmoid_gate(g[rows], want)
+    check_close(got[rows].ravel(), want, "config 5 rows vs oracle (%d rows)" % len(rows))

@@ -25,6 +25,24 @@ def test_reference_api_caller_builds_and_runs(rd4, tmp_path):
     assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout + r.stderr
 
 
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not installed")
+def test_unknown_kv_type_aborts(rd4, tmp_path):
+    """kv_unreachable (kv.h:58-69, checked by check_kvtype.hip:55-75,249-263 with
+    a forked child): a KvType outside the enum kills the caller with SIGABRT
+    instead of returning a guess."""
+    import signal
+    lib = rd4.LIB_PATH
+    exe = str(tmp_path / "shim_caller")
+    cmd = ["g++", "-std=c++17", "-O1", "-D__HIP_PLATFORM_AMD__",
+           "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROCM, "include"),
+           os.path.join(ROOT, "tests", "shim_caller.cpp"), "-o", exe, lib,
+           "-Wl,-rpath," + os.path.dirname(lib)]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    r = subprocess.run([exe, "abort"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == -signal.SIGABRT, (r.returncode, r.stdout, r.stderr)
+    assert "unknown KvType" in r.stderr and "no abort" not in r.stdout
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("hd", [256, 96])
 def test_shim_device_readers_bit_exact(orc, dev, hd):
