@@ -152,6 +152,22 @@ int rd4_attn_decode_append(const float *q, const float *k_new, const float *v_ne
                            void *v, float *out, float *gate, int t, int n_head, int n_head_kv,
                            int head_dim, float scale, int kt, int vt, int n_splits, void *stream);
 
+/* Allocation-free form of rd4_attn_decode_append, same arguments and results
+ * within the attention tolerance (bit-identical at the same split count). No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops). It calls no hipMalloc or
+ * hipFree: its split records live in a fixed 4 MiB device array of the library
+ * (one per GPU, held until the process ends; rd4_init, or the first call on a
+ * device, looks up its address). Shapes whose records exceed it (n_head x
+ * splits x (head_dim + 2) floats > 1M) are refused with RD4_EINVAL when
+ * n_splits is given, and run with fewer splits when it is 0; shapes that take
+ * the generic kernel run one split. Calls that overlap on one GPU (two
+ * streams, or concurrent graph replays) share the array and race. */
+int rd4_attn_decode_append_noalloc(const float *q, const float *k_new, const float *v_new, void *k,
+                                   void *v, float *out, float *gate, int t, int n_head,
+                                   int n_head_kv, int head_dim, float scale, int kt, int vt,
+                                   int n_splits, void *stream);
+
 /* Native multi-token decode (the MTP verify step: N = D+1 drafted tokens,
  * graph.cuh:1494-1527 through attn_split_batch_launch; mtp.cuh:585-596 for the
  * draft token itself): tokens i = 0..n_tok-1 sit at consecutive positions

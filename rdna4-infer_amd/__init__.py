@@ -40,6 +40,7 @@ SIGNATURES = {
     "rd4_attn_split_wpb": ([_I], _I),
     "rd4_attn_decode": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
     "rd4_attn_decode_append": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
+    "rd4_attn_decode_append_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
     "rd4_attn_batch_launch": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P], _I),
     "rd4_attn_split_batch_launch": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
     "rd4_fa2_prefill_launch": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
@@ -163,6 +164,16 @@ def attn_decode_append(q, k_new, v_new, k, v, out, t, n_head, n_head_kv, head_di
     _check(lib().rd4_attn_decode_append(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k), _ptr(v), _ptr(out),
                                         _ptr(gate), t, n_head, n_head_kv, head_dim, scale, kt, vt,
                                         n_splits, _stream()), "attn_decode_append")
+
+
+def attn_decode_append_noalloc(q, k_new, v_new, k, v, out, t, n_head, n_head_kv, head_dim, scale, kt,
+                               vt, gate=None, n_splits=0):
+    """attn_decode_append through the allocation-free entry point (fixed
+    library scratch; calls overlapping on one GPU race)."""
+    _check(lib().rd4_attn_decode_append_noalloc(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k), _ptr(v),
+                                                _ptr(out), _ptr(gate), t, n_head, n_head_kv, head_dim,
+                                                scale, kt, vt, n_splits, _stream()),
+           "attn_decode_append_noalloc")
 
 
 def attn_decode_tokens(q, k, v, out, t0, n_tok, n_head, n_head_kv, head_dim, scale, kt, vt,

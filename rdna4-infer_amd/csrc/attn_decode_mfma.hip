@@ -1704,7 +1704,8 @@ hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hip
   if (a.tok_pair && (a.pos || a.k_new || a.q_f16 || a.n_chunks != 1 || n_tok < 2 ||
                      !pair_type(kt, vt)))
     a.tok_pair = 0;
-  a.ext_merge = (a.n_splits > 1 && (a.tok_pair || decode_mfma_ext_merge())) ? 1 : 0;
+  // (a caller may ask for the merge launch by setting ext_merge beforehand)
+  a.ext_merge = (a.n_splits > 1 && (a.tok_pair || a.ext_merge || decode_mfma_ext_merge())) ? 1 : 0;
   const int grid_tok = a.tok_pair ? (n_tok + 1) / 2 : n_tok;
   hipError_t err = hipErrorInvalidValue;
 #define RD4_D(K, V) \

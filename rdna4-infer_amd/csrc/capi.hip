@@ -140,12 +140,21 @@ int auto_splits(int keys, int ctas_per_split, int target, int min_keys) {
   return s < 1 ? 1 : s;
 }
 
+// Fixed scratch of the allocation-free entry point: records go to `partial`
+// (at most `floats` floats) and are merged by the merge launch.
+struct FixedScratch {
+  float *partial;
+  unsigned *counters;
+  int64_t floats;
+};
+
 // Common body of every decode-style launch.
 int run_attn(const float *q, const void *k, const void *v, float *out, float *gate,
              const int *pos, int t, int n_tok, int n_head, int n_head_kv, int head_dim,
              float scale, int kt, int vt, int splits, hipStream_t st,
              const float *k_new = nullptr, const float *v_new = nullptr, int tok_pair = 0,
-             float *caller_partial = nullptr, int caller_splits = 0) {
+             float *caller_partial = nullptr, int caller_splits = 0,
+             const FixedScratch *fixed = nullptr) {
   int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
   if (rc) return rc;
   if (n_tok < 1) return fail(RD4_EINVAL, "n_tok must be >= 1%s");
@@ -174,6 +183,12 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
     splits = mfma ? auto_splits(t + 1, per_split, 256, 64) : auto_splits(t + 1, per_split, 1024, 64);
     if (splits < min_s) splits = min_s;
   }
+  if (fixed && !mfma) {
+    // the generic kernel merges splits through uncached library scratch: with a
+    // fixed scratch it runs one split, which needs no records
+    if (exact && splits > 1) return fail(RD4_EINVAL, "this shape takes the generic kernel: n_splits must be 0 or 1 here%s");
+    splits = 1;
+  }
   if (splits < 1) splits = 1;
   if (splits > kMaxSplits) {
     if (exact || min_s > kMaxSplits) return fail(RD4_EINVAL, "n_splits above the library's maximum (256)%s");
@@ -196,6 +211,20 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   a.tok_pair = tok_pair;
   if (splits > 1) {
     const int64_t rows = (int64_t)n_tok * n_head;
+    if (fixed) {
+      // records [head][split][hd] + (m, l) must fit; an automatic count shrinks
+      auto fits_fixed = [&](int S) { return rows * S * rec <= fixed->floats; };
+      while (!fits_fixed(splits) && !exact && splits > 1) --splits;
+      if (!fits_fixed(splits))
+        return fail(RD4_EINVAL, "split records exceed the fixed scratch (4 MiB): use fewer splits%s");
+      a.partial = fixed->partial;
+      a.counters = fixed->counters;
+      a.ml0_off = rows * splits * head_dim;
+      a.ext_merge = 1;  // the merge launch: records stay in the fixed scratch, no in-kernel tree
+      a.n_splits = splits;
+      a.dbg = 0;
+      return launched(decode_mfma_launch(kt, vt, a, n_tok, st), "decode kernel");
+    }
     const bool ext = mfma && decode_mfma_ext_merge();
     const bool use_caller = ext && caller_partial && splits <= caller_splits;
     if (!use_caller) {
@@ -253,6 +282,38 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
   return launched(attn_generic_launch(kt, vt, a, n_tok, st), "attention kernel");
 }
 
+// ---- fixed scratch of the allocation-free entry point ------------------------
+// Split records of rd4_attn_decode_append_noalloc live in this file-scope
+// device array (one copy per GPU, held until the process ends). In host code
+// its name is only a stand-in: the device address comes from
+// hipGetSymbolAddress, once per device, and only that address is used.
+// Every record a call reads was written by that call's split kernel, so
+// nothing in it must start at zero.
+constexpr int64_t kFixedFloats = 1 << 20;  // 4 MiB: records of <= 1M floats
+static __device__ __align__(256) float scratch[kFixedFloats];
+
+std::map<int, float *> g_fixed;  // device -> address of `scratch` there
+std::mutex g_fixed_mu;
+
+// Looks up, once per device and with that device current, the address of
+// `scratch` on that device.
+int fixed_scratch(FixedScratch *out) {
+  int dev = 0, rc;
+  if ((rc = current_device(&dev))) return rc;
+  std::lock_guard<std::mutex> lk(g_fixed_mu);
+  auto it = g_fixed.find(dev);
+  if (it == g_fixed.end()) {
+    float *ptr = nullptr;
+    if (hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+      return fail(RD4_ELAUNCH, "hipGetSymbolAddress of the fixed scratch failed%s");
+    it = g_fixed.emplace(dev, ptr).first;
+  }
+  out->partial = it->second;
+  out->counters = nullptr;  // the merge launch uses no counters
+  out->floats = kFixedFloats;
+  return RD4_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -277,7 +338,9 @@ int rd4_init(void) {
     if ((rc = new_scratch(nullptr, true, &n))) return rc;
     sp.push_back(n);
   }
-  return RD4_OK;
+  FixedScratch f;
+  if ((rc = fixed_scratch(&f))) return rc;
+  return hipDeviceSynchronize() == hipSuccess ? RD4_OK : fail(RD4_ELAUNCH, "init sync failed%s");
 }
 
 int rd4_stream_init(void *stream) {
@@ -399,6 +462,23 @@ int rd4_attn_decode_append(const float *q, const float *k_new, const float *v_ne
     return fail(RD4_EINVAL, "cache pointers misaligned%s");
   return run_attn(q, k, v, out, gate, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt, vt,
                   n_splits, (hipStream_t)stream, k_new, v_new);
+}
+
+int rd4_attn_decode_append_noalloc(const float *q, const float *k_new, const float *v_new, void *k,
+                                   void *v, float *out, float *gate, int t, int n_head, int n_head_kv,
+                                   int head_dim, float scale, int kt, int vt, int n_splits, void *stream) {
+  if (n_splits < 0 || t < 0 || !k_new || !v_new)
+    return fail(RD4_EINVAL, "append needs t >= 0, n_splits >= 0 and both new rows%s");
+  if ((((uintptr_t)k_new) | ((uintptr_t)v_new)) & 15)
+    return fail(RD4_EINVAL, "new rows must be 16-byte aligned%s");
+  int rc = check_attn_shape(n_head, n_head_kv, head_dim, kt, vt);
+  if (rc) return rc;
+  if ((kt >= RD4_KV_Q8_0 && ((uintptr_t)k & 1)) || (vt >= RD4_KV_Q8_0 && ((uintptr_t)v & 1)))
+    return fail(RD4_EINVAL, "cache pointers misaligned%s");
+  FixedScratch f;
+  if ((rc = fixed_scratch(&f))) return rc;
+  return run_attn(q, k, v, out, gate, nullptr, t, 1, n_head, n_head_kv, head_dim, scale, kt, vt,
+                  n_splits, (hipStream_t)stream, k_new, v_new, 0, nullptr, 0, &f);
 }
 
 int rd4_attn_decode_tokens(const float *q, const void *k, const void *v, float *out, float *gate,
