@@ -807,7 +807,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   const int tcta = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
 #define RD4_TP()                                                                          \
   do {                                                                                    \
-    if (lane == 0 && tpos < 32 && tcta < 1024)                                            \
+    if (lane == 0 && tpos < 28 && tcta < 1024)                                            \
       rd4_dec_trace[(tcta * 8 + w) * 32 + tpos++] = __builtin_amdgcn_s_memrealtime();     \
   } while (0)
 #else
@@ -1625,6 +1625,10 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         }
         a.out[oi] = o1;
       }
+    } else if (!pair && a.mrec) {
+      // in-kernel slice merge: the record goes to the slice that holds (hh, d)
+      slice_record_store(a, ((tok * a.n_head_kv + kvh) * a.n_chunks + hc), s, hh * kHD + d, kHD,
+                         make_float4(acc4[0], acc4[1], acc4[2], acc4[3]), mm, L);
     } else {
       *(floatx4 *)(rec_acc(a, hrow_r, s) + d) = acc4;
       if (d == 0) {
@@ -1636,6 +1640,15 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   }
   RD4_TP();
   if (a.n_splits == 1) return;
+  if (!pair && a.mrec) {
+#if RD4_DEC_TRACE
+    slice_merge<kThreads>(a, (tok * a.n_head_kv + kvh) * a.n_chunks + hc, tok, h0, G, s, ms,
+                          tcta < 1024 ? &rd4_dec_trace[(tcta * 8 + w) * 32] : nullptr);
+#else
+    slice_merge<kThreads>(a, (tok * a.n_head_kv + kvh) * a.n_chunks + hc, tok, h0, G, s, ms);
+#endif
+    return;
+  }
   int *flag = (int *)(ms + 2 * kR + kWaves * kR);
   if (pair || a.ext_merge || (a.dbg & 1)) return;
   split_tail<kThreads>(a, tok, kvh, hc, h0, G, s, flag, (float *)(flag + 4),
@@ -1650,8 +1663,10 @@ size_t decode_lds() {
   // query rows (later the shared fragments and the q4_1 block sums)
   const size_t qreg = (size_t)kG * (kHD * 4 + 16) + 256 + TS::QI;
   const size_t tiles = (size_t)TS::WAVES * TS::R * TS::TB + qreg;  // scale tables are static LDS
-  const size_t merge = (2 * TS::WAVES * 16 + TS::WAVES * 16 * kRowPad + 2 * 16 + TS::WAVES * 16 + 4) * 4 +
-                       (kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
+  // (past the wave states: the in-kernel tree's flag and tables, or the slice
+  // merge's 64 (m, l) quads)
+  const size_t tail = (2 * 16 + TS::WAVES * 16 + 4 + kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
+  const size_t merge = (2 * TS::WAVES * 16 + TS::WAVES * 16 * kRowPad) * 4 + (tail > 1040 ? tail : 1040);
   return tiles > merge ? tiles : merge;
 }
 
@@ -1705,7 +1720,8 @@ hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hip
                      !pair_type(kt, vt)))
     a.tok_pair = 0;
   // (a caller may ask for the merge launch by setting ext_merge beforehand)
-  a.ext_merge = (a.n_splits > 1 && (a.tok_pair || a.ext_merge || decode_mfma_ext_merge())) ? 1 : 0;
+  if (a.tok_pair) a.mrec = nullptr;  // pair CTAs hand their records to the merge launch
+  a.ext_merge = (a.n_splits > 1 && !a.mrec && (a.tok_pair || a.ext_merge || decode_mfma_ext_merge())) ? 1 : 0;
   const int grid_tok = a.tok_pair ? (n_tok + 1) / 2 : n_tok;
   hipError_t err = hipErrorInvalidValue;
 #define RD4_D(K, V) \

@@ -58,6 +58,12 @@ constexpr int kKBytes = kBN * kHD * 2;     // K block, 32 KiB
 constexpr int kKStages = 3, kVStages = 2;
 constexpr int kLdsBytes = (kKStages + kVStages) * kKBytes;
 constexpr float kLog2e = 1.4426950408889634f;
+// profiling knob bits of prefill_mfma_kernel (0 in production builds): 1 no K
+// fragment reads, 2 no V fragment reads, 4 no softmax, 8 no DMA after the
+// first blocks, 16 no block barrier, 32 no MFMA, 64 no key blocks at all
+#ifndef RD4_PF_KNOB
+#define RD4_PF_KNOB 0
+#endif
 
 __device__ __forceinline__ _Float16 h16(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
@@ -142,7 +148,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
     for (int m = 1; m < 64; m <<= 1) lim = max(lim, __shfl_xor(lim, m, 64));
     kend = __builtin_amdgcn_readfirstlane(lim);
   }
-  const int n_blocks = (kend + kBN) / kBN;
+  const int n_blocks = (RD4_PF_KNOB & 64) ? 0 : (kend + kBN) / kBN;
 
   const int64_t kvstride = (int64_t)p.n_head_kv * kHD * 2;  // bytes between consecutive keys
   const uint8_t *kbase = p.k + (int64_t)kvh * kHD * 2;
@@ -293,49 +299,58 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
     // every wave's DMA for blk landed; every wave is done with blk - 1. A CTA
     // barrier for LDS only: __syncthreads would also wait for K(blk + 1).
 #ifndef RD4_PF_FULLBAR
-    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (!(RD4_PF_KNOB & 16)) __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #else
     __syncthreads();
 #endif
-    if (blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
-    if (blk + 2 < n_blocks) issue_k(blk + 2, ks == 0 ? 2 : ks - 1);  // (blk + 2) % 3
+    if (!(RD4_PF_KNOB & 8)) {
+      if (blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
+      if (blk + 2 < n_blocks) issue_k(blk + 2, ks == 0 ? 2 : ks - 1);  // (blk + 2) % 3
+    }
     const uint8_t *kd = smem + ks * kKBytes;
     const uint8_t *vd = smem + (kKStages + vs) * kKBytes;
     ks = ks == 2 ? 0 : ks + 1;
     const int j0 = blk * kBN;
     const bool need_mask = (j0 + kBN - 1) > wave_min_lim;
 
-    // ---- S^T for 4 key tiles x 2 slabs; the next tile's K fragments are read
-    // from LDS while the current tile's MFMAs run.
+    // ---- S^T for 4 key tiles x the wave's slabs; the next tile's K fragments
+    // are read from LDS while the current tile's MFMAs run.
     floatx4 s[kNSL][4];
+#pragma unroll
+    for (int sl = 0; sl < kNSL; ++sl)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) s[sl][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
     // fragment f = 8*kt + b of the block: key tile kt, 32-dim step b; a ring of
     // 2 x 4 fragments keeps the next four reads in flight behind four MFMA pairs
     u32x4 kb[2][4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) kb[0][b] = *(const u32x4 *)(kd + k_loff[b]);
+    for (int b = 0; b < 4; ++b) kb[0][b] = (RD4_PF_KNOB & 1) ? __builtin_bit_cast(u32x4, qf[0][b]) : *(const u32x4 *)(kd + k_loff[b]);
 #pragma unroll
     for (int h = 0; h < 8; ++h) {  // half-tile h: kt = h/2, b = 4*(h&1) .. +3
       if (h < 7) {
         const int kt1 = (h + 1) >> 1, b1 = 4 * ((h + 1) & 1);
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          kb[(h + 1) & 1][b] = *(const u32x4 *)(kd + kt1 * 16 * (kHD * 2) + k_loff[b1 + b]);
+          kb[(h + 1) & 1][b] = (RD4_PF_KNOB & 1) ? __builtin_bit_cast(u32x4, qf[0][(b + h) & 7]) : *(const u32x4 *)(kd + kt1 * 16 * (kHD * 2) + k_loff[b1 + b]);
       }
       const int kt = h >> 1, b0 = 4 * (h & 1);
-      if (b0 == 0) {
-#pragma unroll
-        for (int sl = 0; sl < kNSL; ++sl) s[sl][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      }
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const half8 kf = __builtin_bit_cast(half8, kb[h & 1][b]);
 #pragma unroll
         for (int sl = 0; sl < kNSL; ++sl)
-          s[sl][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][b0 + b], s[sl][kt], 0, 0, 0);
+          s[sl][kt] = (RD4_PF_KNOB & 32) ? s[sl][kt] + (float)kf[0]
+                      : __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][b0 + b], s[sl][kt], 0, 0, 0);
       }
     }
     // ---- online softmax per slab: lane = row n, keys 16kt + 4g + i
     half8 pf[kNSL][2];
+    if (RD4_PF_KNOB & 4) {
+#pragma unroll
+      for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pf[0][kg][i] = (_Float16)s[0][2 * kg + (i >> 2)][i & 3];
+    } else
 #pragma unroll
     for (int sl = 0; sl < kNSL; ++sl) {
       float tmax = -INFINITY;
@@ -388,6 +403,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
           const uint8_t *a0 = vd + (32 * kg) * (kHD * 2) + tr_off + ((32 * (dt0 + d)) ^ tr_m);
+          if (RD4_PF_KNOB & 2) {
+            vb[buf][d] = qf[0][(dt0 + d) & 7];
+            continue;
+          }
           const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4 *)a0);
           const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4 *)(a0 + 16 * (kHD * 2)));
           vb[buf][d] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -402,7 +421,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
           const int dt = 2 * q2 + d;
 #pragma unroll
           for (int sl = 0; sl < kNSL; ++sl)
-            o[sl][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb[q2 & 1][d], pf[sl][kg], o[sl][dt], 0, 0, 0);
+            o[sl][dt] = (RD4_PF_KNOB & 32) ? o[sl][dt] + (float)vb[q2 & 1][d][0]
+                        : __builtin_amdgcn_mfma_f32_16x16x32_f16(vb[q2 & 1][d], pf[sl][kg], o[sl][dt], 0, 0, 0);
         }
       }
     }

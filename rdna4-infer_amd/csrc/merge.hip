@@ -16,45 +16,6 @@ namespace {
 
 constexpr int kQuarterDims = 64;
 
-// Lane exchanges without LDS round trips: DPP within 16-lane rows (xor 1, xor 2,
-// then the half-row and row mirrors, which pair the 4- and 8-lane groups), and
-// the gfx950 row / half-wave swaps for lanes ^ 16 and ^ 32 (asm with tied
-// operands; s_nop 1 covers the VALU-write -> swap-read hazard).
-__device__ __forceinline__ float dpp_f(float x, int ctrl_sel) {
-  const int v = __builtin_bit_cast(int, x);
-  int r;
-  switch (ctrl_sel) {  // the DPP control must be a constant
-    case 0: r = __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
-    case 1: r = __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false); break;   // quad_perm 2,3,0,1
-    case 2: r = __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
-    default: r = __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false); break; // row_mirror
-  }
-  return __builtin_bit_cast(float, r);
-}
-__device__ __forceinline__ void swap16(float &a, float &b) {
-  __asm__("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap32(float &a, float &b) {
-  __asm__("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c) x = fmaxf(x, dpp_f(x, c));
-  float a = x, b = x;
-  swap16(a, b);
-  float c = fmaxf(a, b), d = c;
-  swap32(c, d);
-  return fmaxf(c, d);
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c) x += dpp_f(x, c);
-  float a = x, b = x;
-  swap16(a, b);
-  float c = a + b, d = c;
-  swap32(c, d);
-  return c + d;
-}
 // x summed over lanes l, l ^ 16, l ^ 32, l ^ 48
 __device__ __forceinline__ float sum_groups4(float x) {
   float a = x, b = x;

@@ -302,12 +302,13 @@ print("ok")
         assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
 
 
-def test_in_kernel_merge_tree_env():
+@pytest.mark.parametrize("mode", ["2", "3"])
+def test_in_kernel_merge_env(mode):
     """RD4_DECODE_MERGE=2 selects the in-kernel counter-tree merge of the split
-    records instead of the merge launch (kept for comparison). Both must match
-    the oracle, over one merge level (16 splits) and two (64 splits), and repeat
-    bit for bit (the counters reset themselves). Child process: the library reads
-    the variable once."""
+    records instead of the merge launch, 3 the in-kernel slice merge (both kept
+    for comparison). Each must match the oracle at 16 and 64 splits and repeat
+    bit for bit (the tree's counters reset themselves; the slice merge restores
+    its poison pattern). Child process: the library reads the variable once."""
     import subprocess
     import sys
     import os
@@ -334,12 +335,12 @@ for kt, vt in ((2, 2), (3, 3), (1, 1)):
             rd4.attn_decode(q, k, v, o, n - 1, nh, nkv, hd, 1 / 16, kt, vt, n_splits=splits)
             torch.cuda.synchronize()
             outs.append(o.cpu().numpy())
-        check_close(outs[0], want, "tree %d/%d splits %d" % (kt, vt, splits))
+        check_close(outs[0], want, "merge %d/%d splits %d" % (kt, vt, splits))
         assert np.array_equal(outs[0], outs[1]), "repeat differs"
 print("ok")
 '''
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    env = dict(os.environ, RD4_DECODE_MERGE="2")
+    env = dict(os.environ, RD4_DECODE_MERGE=mode)
     r = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True, text=True,
                        timeout=180)
     assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr

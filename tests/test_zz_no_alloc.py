@@ -2,7 +2,9 @@
 against the entry point it mirrors (rd4_attn_decode_append): same kernels, its
 split records in the library's fixed device array. Two calls in a row, the
 second on a smaller input, each checked against the allocating entry point on
-identical inputs and against the f64 oracle."""
+identical inputs and against the f64 oracle. (The allocating entry point
+merges the splits inside its launch, the allocation-free one in a merge
+launch; the summation orders differ, so the bar is the attention tolerance.)"""
 import numpy as np
 import pytest
 
@@ -44,8 +46,7 @@ def test_noalloc_two_calls_second_smaller(rd4, orc, dev):
     # scratch on first use; the allocation-free one allocates nothing
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
-        o0, o1 = _case(rd4, orc, dev, 2, 2, 8192, 300)          # q8_0, 64 splits
-        assert np.array_equal(o0, o1)                           # same kernels, same split count
+        _case(rd4, orc, dev, 2, 2, 8192, 300)                   # q8_0, 64 splits
         _case(rd4, orc, dev, 1, 3, 700, 310)                    # smaller: f16 K / q4_0 V, 11 splits
         _case(rd4, orc, dev, 0, 0, 300, 320)                    # generic kernel, one split
         torch.cuda.synchronize()
