@@ -45,12 +45,7 @@ typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
 
 constexpr int kHD = 256;
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kNSL = 1;                    // 16-row MFMA slabs per wave
-constexpr int kRowsW = 16 * kNSL;          // rows per wave
-constexpr int kNDMA = 2048 / (64 * kWaves); // 16-byte DMA chunks per lane per K (or V) block
-constexpr int kBM = kWaves * kRowsW;       // rows per CTA
+constexpr int kBM = 128;                   // rows per CTA
 constexpr int kBN = 64;                    // keys per block
 constexpr int kKBytes = kBN * kHD * 2;     // K block, 32 KiB
 // LDS: three K stages then two V stages (the whole 160 KiB): K streams two
@@ -81,7 +76,12 @@ __device__ __forceinline__ float max_groups4(float x) {
 
 }  // namespace
 
-__global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p) {
+// W waves of NSL 16-row slabs each (W * 16 * NSL = 128 rows per CTA).
+template <int W, int NSL>
+__global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) {
+  constexpr int kRowsWT = 16 * NSL;         // rows per wave
+  constexpr int ND = 2048 / (64 * W);       // 16-byte DMA chunks per lane per K (or V) block
+  static_assert(W * kRowsWT == kBM, "a CTA holds 128 rows");
   extern __shared__ __align__(16) uint8_t smem[];
   // the wave index is uniform: readfirstlane keeps DMA bases and LDS
   // destinations in scalar registers
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   if (p.app_k) {
     const int nrow = p.n_q * p.n_head_kv, total_rows = 2 * nrow;
     const int rb_bytes = (int)row_bytes(p.app_type, kHD);
-    for (int R = (int)blockIdx.x * kWaves + w; R < total_rows; R += (int)gridDim.x * kWaves) {
+    for (int R = (int)blockIdx.x * W + w; R < total_rows; R += (int)gridDim.x * W) {
       const bool isv = R >= nrow;
       const int rr = isv ? R - nrow : R;
       const float4 x4 = *(const float4 *)((isv ? p.app_v_src : p.app_k_src) + (int64_t)rr * kHD + 4 * lane);
@@ -158,11 +158,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   // r0 + 32w + 16s + n), f16 (f32 queries are rounded to f16)
   // q is pre-scaled by scale*log2(e) so S comes out in the exp2 domain
   const float sl2 = p.scale * kLog2e;
-  half8 qf[kNSL][8];
-  int lim_row[kNSL];
+  half8 qf[NSL][8];
+  int lim_row[NSL];
 #pragma unroll
-  for (int sl = 0; sl < kNSL; ++sl) {
-    const int row = r0 + kRowsW * w + 16 * sl + n;
+  for (int sl = 0; sl < NSL; ++sl) {
+    const int row = r0 + kRowsWT * w + 16 * sl + n;
     lim_row[sl] = limit_of(row);
     const bool on = row < n_rows;
     const int q = on ? row / grp : 0;
@@ -197,18 +197,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   // The wave's smallest row limit: blocks whose last key is <= it need no mask.
   int wave_min_lim = lim_row[0];
 #pragma unroll
-  for (int sl = 1; sl < kNSL; ++sl) wave_min_lim = min(wave_min_lim, lim_row[sl]);
+  for (int sl = 1; sl < NSL; ++sl) wave_min_lim = min(wave_min_lim, lim_row[sl]);
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) wave_min_lim = min(wave_min_lim, __shfl_xor(wave_min_lim, m, 64));
 
-  floatx4 o[kNSL][16];
+  floatx4 o[NSL][16];
 #pragma unroll
-  for (int sl = 0; sl < kNSL; ++sl)
+  for (int sl = 0; sl < NSL; ++sl)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[sl][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run[kNSL], l_run[kNSL];
+  float m_run[NSL], l_run[NSL];
 #pragma unroll
-  for (int sl = 0; sl < kNSL; ++sl) {
+  for (int sl = 0; sl < NSL; ++sl) {
     m_run[sl] = -INFINITY;
     l_run[sl] = 0.0f;
   }
@@ -216,10 +216,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   // ---- block loads. K: 2048 chunks of 16 B per block = 8 DMA instructions per
   // lane; chunk c -> key c/32, LDS slot c%32 holds global column slot^(key&15).
   // Per-lane offsets are block-invariant and computed once.
-  uint32_t k_goff[kNDMA];  // byte offset of this lane's chunk r from the block's first key (scalar base + 32-bit vector offset)
+  uint32_t k_goff[ND];  // byte offset of this lane's chunk r from the block's first key (scalar base + 32-bit vector offset)
 #pragma unroll
-  for (int r = 0; r < kNDMA; ++r) {
-    const int c = (w * kNDMA + r) * 64 + lane;
+  for (int r = 0; r < ND; ++r) {
+    const int c = (w * ND + r) * 64 + lane;
     const int key = c >> 5, slot = c & 31;
     k_goff[r] = (uint32_t)(key * (int)kvstride + 16 * (slot ^ (key & 15)));
   }
@@ -229,18 +229,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
     const uint8_t *src = kbase + (int64_t)j0 * kvstride;
     if (j0 + kBN - 1 <= kend) {
 #pragma unroll
-      for (int r = 0; r < kNDMA; ++r)
+      for (int r = 0; r < ND; ++r)
         __builtin_amdgcn_global_load_lds((const void *)(src + k_goff[r]),
-                                         (lds_void *)(kd + (w * kNDMA + r) * 1024), 16, 0, 0);
+                                         (lds_void *)(kd + (w * ND + r) * 1024), 16, 0, 0);
     } else {  // last block: keys past kend re-read a valid row (masked later)
 #pragma unroll
-      for (int r = 0; r < kNDMA; ++r) {
-        const int c = (w * kNDMA + r) * 64 + lane;
+      for (int r = 0; r < ND; ++r) {
+        const int c = (w * ND + r) * 64 + lane;
         const int key = c >> 5, slot = c & 31;
         const int jk = min(j0 + key, kend);
         __builtin_amdgcn_global_load_lds(
             (const void *)(kbase + (int64_t)jk * kvstride + 16 * (slot ^ (key & 15))),
-            (lds_void *)(kd + (w * kNDMA + r) * 1024), 16, 0, 0);
+            (lds_void *)(kd + (w * ND + r) * 1024), 16, 0, 0);
       }
     }
   };
@@ -251,18 +251,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
     const uint8_t *src = vbase + (int64_t)j0 * kvstride;
     if (j0 + kBN - 1 <= kend) {
 #pragma unroll
-      for (int r = 0; r < kNDMA; ++r)
+      for (int r = 0; r < ND; ++r)
         __builtin_amdgcn_global_load_lds((const void *)(src + k_goff[r]),
-                                         (lds_void *)(vd + (w * kNDMA + r) * 1024), 16, 0, 0);
+                                         (lds_void *)(vd + (w * ND + r) * 1024), 16, 0, 0);
     } else {
 #pragma unroll
-      for (int r = 0; r < kNDMA; ++r) {
-        const int c = (w * kNDMA + r) * 64 + lane;
+      for (int r = 0; r < ND; ++r) {
+        const int c = (w * ND + r) * 64 + lane;
         const int key = c >> 5, slot = c & 31;
         const int jk = min(j0 + key, kend);
         __builtin_amdgcn_global_load_lds(
             (const void *)(vbase + (int64_t)jk * kvstride + 16 * (slot ^ (key & 15))),
-            (lds_void *)(vd + (w * kNDMA + r) * 1024), 16, 0, 0);
+            (lds_void *)(vd + (w * ND + r) * 1024), 16, 0, 0);
       }
     }
   };
@@ -291,8 +291,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int vs = blk & 1;
     if (blk + 1 < n_blocks) {
-      static_assert(kNDMA == 4, "vmcnt below counts one K block's DMA instructions");
-      __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory");  // K(j), V(j) landed; K(j+1) may fly
+      // K(j), V(j) landed; K(j+1) (its ND DMA instructions) may fly
+      __builtin_amdgcn_s_waitcnt((ND & 15) | ((ND >> 4) << 14) | (7 << 4) | (15 << 8));
     } else {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
@@ -315,9 +315,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 
     // ---- S^T for 4 key tiles x the wave's slabs; the next tile's K fragments
     // are read from LDS while the current tile's MFMAs run.
-    floatx4 s[kNSL][4];
+    floatx4 s[NSL][4];
 #pragma unroll
-    for (int sl = 0; sl < kNSL; ++sl)
+    for (int sl = 0; sl < NSL; ++sl)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) s[sl][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
     // fragment f = 8*kt + b of the block: key tile kt, 32-dim step b; a ring of
@@ -338,13 +338,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
       for (int b = 0; b < 4; ++b) {
         const half8 kf = __builtin_bit_cast(half8, kb[h & 1][b]);
 #pragma unroll
-        for (int sl = 0; sl < kNSL; ++sl)
+        for (int sl = 0; sl < NSL; ++sl)
           s[sl][kt] = (RD4_PF_KNOB & 32) ? s[sl][kt] + (float)kf[0]
                       : __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][b0 + b], s[sl][kt], 0, 0, 0);
       }
     }
     // ---- online softmax per slab: lane = row n, keys 16kt + 4g + i
-    half8 pf[kNSL][2];
+    half8 pf[NSL][2];
     if (RD4_PF_KNOB & 4) {
 #pragma unroll
       for (int kg = 0; kg < 2; ++kg)
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
         for (int i = 0; i < 8; ++i) pf[0][kg][i] = (_Float16)s[0][2 * kg + (i >> 2)][i & 3];
     } else
 #pragma unroll
-    for (int sl = 0; sl < kNSL; ++sl) {
+    for (int sl = 0; sl < NSL; ++sl) {
       float tmax = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -420,7 +420,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
         for (int d = 0; d < 2; ++d) {
           const int dt = 2 * q2 + d;
 #pragma unroll
-          for (int sl = 0; sl < kNSL; ++sl)
+          for (int sl = 0; sl < NSL; ++sl)
             o[sl][dt] = (RD4_PF_KNOB & 32) ? o[sl][dt] + (float)vb[q2 & 1][d][0]
                         : __builtin_amdgcn_mfma_f32_16x16x32_f16(vb[q2 & 1][d], pf[sl][kg], o[sl][dt], 0, 0, 0);
         }
@@ -430,11 +430,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_mfma_kernel(PrefillArgs p
 
   // ---- epilogue: l over the 4 key groups, normalize, gate, store
 #pragma unroll
-  for (int sl = 0; sl < kNSL; ++sl) {
+  for (int sl = 0; sl < NSL; ++sl) {
     float L = l_run[sl];
     L += __shfl_xor(L, 16, 64);
     L += __shfl_xor(L, 32, 64);
-    const int row = r0 + kRowsW * w + 16 * sl + n;
+    const int row = r0 + kRowsWT * w + 16 * sl + n;
     if (row >= n_rows) continue;
     const int q = row / grp, head = kvh * grp + row % grp;
     const float inv = (m_run[sl] == -INFINITY || !(L > 0.0f)) ? 0.0f : 1.0f / L;
@@ -468,7 +468,14 @@ hipError_t prefill_mfma_launch(const PrefillArgs &p, hipStream_t st) {
   const int grp = p.n_head / p.n_head_kv;
   const int n_rb = (p.n_q * grp + kBM - 1) / kBM;
   dim3 grid((unsigned)(n_rb * p.n_head_kv));
-  hipLaunchKernelGGL(prefill_mfma_kernel, grid, dim3(kThreads), (size_t)kLdsBytes, st, p);
+  static const int shape = [] {
+    const char *e = std::getenv("RD4_PREFILL_SHAPE");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (shape == 1)  // 4 waves x 32 rows (one wave per SIMD)
+    hipLaunchKernelGGL((prefill_mfma_kernel<4, 2>), grid, dim3(256), (size_t)kLdsBytes, st, p);
+  else  // 8 waves x 16 rows (two waves per SIMD)
+    hipLaunchKernelGGL((prefill_mfma_kernel<8, 1>), grid, dim3(512), (size_t)kLdsBytes, st, p);
   return hipGetLastError();
 }
 
