@@ -15,7 +15,10 @@ Default run: both halves of the headline metric in one JSON line.
   f16 keys, causal, gated, with the chunk's K/V rows appended as q8_0 in the
   same rd4_prefill_append launch.
 
-value = algorithmic bytes of a step / step time (GB/s). Each roofline object
+value = algorithmic bytes of a step / step time (GB/s). "hbm_read_ceiling" is
+the same run's measurement of a launch that only streams the same bytes
+(rd4_read_probe, 16 HBM-true launches per step): the practical ceiling beside
+the 8 TB/s peak. Each roofline object
 covers that half's dominant kernel, timed with HIP events on the stream the
 library launches on. cpu_baseline = the scalar CPU oracle (f64, one thread) on
 a bounded sample of the same workload. `--workload X` measures one workload
@@ -297,6 +300,28 @@ def prefill_result(rd4, args, torch):
             "config": info, "roofline": roof}, cpu
 
 
+def read_ceiling(rd4, args, torch, steps=None):
+    """Practical HBM read rate for the decode step's traffic: one streaming-read
+    launch (rd4_read_probe: loads only) per layer over a buffer of a q8_0 32K
+    layer's K+V bytes, `args.layers` distinct buffers (larger than the MALL),
+    replayed as a HIP graph exactly like the decode step."""
+    nbytes = 32768 * NKV * 272 * 2
+    bufs = [torch.full((nbytes,), l, dtype=torch.uint8, device="cuda") for l in range(args.layers)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+
+    def step():
+        for b in bufs:
+            rd4.read_probe(b, sink)
+    run = as_graph(torch, step) or step
+    wall_ms, _ = measure(torch, run, run, steps or args.steps, args.warmup)
+    gbs = nbytes * args.layers / (wall_ms * 1e-3) / 1e9
+    del bufs
+    torch.cuda.empty_cache()
+    return {"bytes_per_launch": nbytes, "launches_per_step": args.layers,
+            "us_per_launch": round(wall_ms * 1e3 / args.layers, 3), "GB/s": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def build_workload(torch, rd4, name, args):
     layers = args.layers
     if name == "decode_q8_0":
@@ -327,7 +352,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "decode_q8_0", "decode_f16", "decode_q4_0", "decode_q5_0_q4_1",
-                             "decode_tokens", "prefill", "copy"])
+                             "decode_tokens", "prefill", "copy", "read"])
     ap.add_argument("--layers", type=int, default=16,
                     help="attention layers (each with its own cache) per decode step")
     ap.add_argument("--eager", action="store_true", help="launch the decode step eagerly, no graph")
@@ -343,6 +368,10 @@ def main():
     rd4.lib()
     if rd4.lib().rd4_init() != 0:
         raise SystemExit("rd4_init failed: " + rd4.lib().rd4_last_error().decode())
+
+    if args.workload == "read":
+        print(json.dumps(dict(read_ceiling(rd4, args, torch), workload="read")))
+        return
 
     if args.workload == "copy":
         # Plain device copy of a known size: the calibration run for the
@@ -390,9 +419,17 @@ def main():
            "roofline": r["roofline"]}
     if not args.no_cpu and cpu is not None:
         res.update(cpu_fields(cpu, "GB/s", True))
+    if name == "decode_q8_0":
+        # what a launch that only streams the same bytes reaches on this GPU, in
+        # the same run: the practical ceiling next to the 8 TB/s peak
+        del cpu
+        torch.cuda.empty_cache()
+        ceil = read_ceiling(rd4, args, torch)
+        ceil["decode_frac_of_ceiling"] = round(r["roofline"]["achieved"] / ceil["GB/s"], 4)
+        res["hbm_read_ceiling"] = ceil
+        cpu = None
     if args.workload == "headline":
         # the metric's second half: configs[4] prefill, measured in the same run
-        del cpu
         torch.cuda.empty_cache()
         p, pcpu = prefill_result(rd4, args, torch)
         if not args.no_cpu:

@@ -273,6 +273,14 @@ int rd4_qk_norm_rope_append(const float *qg, const float *k_new, const float *v_
                             int head_dim, float *q_out, float *gate_out, float *k_out, void *k,
                             void *v, int kt, int vt, void *stream);
 
+/* ---- diagnostics ------------------------------------------------------------ */
+
+/* Streaming read of `bytes` bytes (16-byte aligned, a multiple of 16) by one
+ * launch that only loads and discards (sink: a device word written only in an
+ * unlikely case). Used by bench.py to measure the practical HBM read rate of a
+ * decode-sized launch; no counterpart in the reference. */
+int rd4_read_probe(const void *buf, int64_t bytes, void *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,7 @@ SIGNATURES = {
     "rd4_sigmoid_gate_launch": ([_P, _P, _I64, _P], _I),
     "rd4_rope_launch": ([_P, _I, _I, _I, _I, _F, _P, _P], _I),
     "rd4_attn_decode_tokens": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P], _I),
+    "rd4_read_probe": ([_P, _I64, _P, _P], _I),
     "rd4_rms_norm_launch": ([_P, _P, _P, _I64, _I64, _F, _P], _I),
     "rd4_qk_norm_rope_append": ([_P, _P, _P, _P, _P, _F, _I, _F, _P, _I, _I, _I, _I, _P, _P, _P,
                                  _P, _P, _I, _I, _P], _I),
@@ -289,3 +290,9 @@ def stream_init(stream=None):
 
 def attn_partial_bytes(n_head, head_dim, n_splits):
     return int(lib().rd4_attn_partial_bytes(n_head, head_dim, n_splits))
+
+
+def read_probe(buf, sink):
+    """rd4_read_probe: one streaming-read launch over the bytes of `buf` (bench calibration)."""
+    _check(lib().rd4_read_probe(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink), _stream()),
+           "read_probe")

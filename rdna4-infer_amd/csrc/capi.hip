@@ -20,6 +20,7 @@ hipError_t kv_fill_launch(int t, uint8_t *dst, int64_t n, uint32_t seed, hipStre
 hipError_t kv_load_launch(int t, const uint8_t *src, float *dst, int64_t n, hipStream_t st);
 hipError_t sigmoid_gate_launch(float *g, float *y, int64_t n, hipStream_t st);
 hipError_t fill_u32_launch(uint32_t *p, int64_t n, uint32_t v, hipStream_t st);
+hipError_t read_probe_launch(const void *p, int64_t bytes, uint32_t *sink, hipStream_t st);
 hipError_t rope_launch(float *x, int n_tokens, int n_heads, int head_dim, int n_rot,
                        float freq_base, const int *pos, hipStream_t st);
 hipError_t rms_norm_launch(const float *x, const float *w, float *y, int64_t nrows, int64_t ncols,
@@ -697,6 +698,13 @@ int rd4_prefill_append(const void *q, int q_f16, const void *k, const void *v, f
   p.app_v = (uint8_t *)v_dst;
   p.app_type = dst_type;
   return launched(prefill_launch(kt, vt, p, (hipStream_t)stream), "prefill");
+}
+
+int rd4_read_probe(const void *buf, int64_t bytes, void *sink, void *stream) {
+  if (bytes < 0 || (bytes > 0 && (!buf || !sink)) || ((uintptr_t)buf & 15) || (bytes & 15) ||
+      ((uintptr_t)sink & 3))
+    return fail(RD4_EINVAL, "read probe needs a 16-byte aligned buffer, a multiple of 16 bytes and a sink%s");
+  return launched(read_probe_launch(buf, bytes, (uint32_t *)sink, (hipStream_t)stream), "read probe");
 }
 
 int rd4_sigmoid_gate_launch(float *g_io, float *y_io, int64_t n, void *stream) {
