@@ -411,10 +411,9 @@ __device__ __forceinline__ void slice_merge(const AttnArgs &a, int gi, int tok, 
     }
   }
   if (trace && lane == 0) trace[30] = __builtin_amdgcn_s_memrealtime();
-  // every wave has read its quads (and the shared (m, l)): restore kPoison
-  // (LDS-only barrier: the reads have completed; a plain one would also wait
-  // for the output stores)
-  __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // restore kPoison over what this wave read from memory: its value quads, and
+  // for wave 0 the (m, l) quads (the other waves took (m, l) from LDS), so no
+  // barrier is needed first
   if (on) {
     const float pz = __builtin_bit_cast(float, kPoison);
     const float4 pz4 = make_float4(pz, pz, pz, pz);
