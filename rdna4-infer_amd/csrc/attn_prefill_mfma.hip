@@ -59,6 +59,42 @@ constexpr float kLog2e = 1.4426950408889634f;
 #ifndef RD4_PF_KNOB
 #define RD4_PF_KNOB 0
 #endif
+// operand ring depth of the PV phase (steps of two MFMAs whose V^T operands
+// are in registers or in flight)
+#ifndef RD4_PF_PVD
+#define RD4_PF_PVD 3
+#endif
+constexpr int kPVD = RD4_PF_PVD;
+// QK^T operand ring: kQD steps of kQG K fragments
+#ifndef RD4_PF_QKG
+#define RD4_PF_QKG 2
+#endif
+#ifndef RD4_PF_QKD
+#define RD4_PF_QKD 4
+#endif
+constexpr int kQG = RD4_PF_QKG, kQD = RD4_PF_QKD;
+// scheduling fences (experiment): 1 after each QK^T step, 2 after each PV step,
+// so the operand reads stay as far ahead of their MFMAs as written
+#ifndef RD4_PF_SB
+#define RD4_PF_SB 7
+#endif
+// the first PV operand reads go out before the softmax (1) or after it (0)
+#ifndef RD4_PF_VEARLY
+#define RD4_PF_VEARLY 1
+#endif
+// causal mask under a wave-uniform branch (1) or applied to every block (0)
+#ifndef RD4_PF_MASKBR
+#define RD4_PF_MASKBR 1
+#endif
+#ifndef RD4_PF_PRIO
+#define RD4_PF_PRIO 0
+#endif
+// wave priority around the MFMA phases (experiment): 1 raises it for the QK^T and
+// PV phases of every wave, 2 only for the first wave of each SIMD
+template <int V>
+__device__ __forceinline__ void pf_prio(int w) {
+  if (RD4_PF_PRIO == 1 || (RD4_PF_PRIO == 2 && w < 4)) __builtin_amdgcn_s_setprio(V);
+}
 
 __device__ __forceinline__ _Float16 h16(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
@@ -72,6 +108,21 @@ __device__ __forceinline__ float max_groups4(float x) {
   float c = fmaxf(a, b), d = c;
   __asm__("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
   return fmaxf(c, d);
+}
+
+// LDS swizzle of a K/V row: 16-byte chunk c of key r sits in slot c ^ swz(r).
+// swz is the GF(2)-linear map with r's bits 0..3 -> 8, 7, 2, 4 (a permutation
+// of 0..15). Plain r & 15 leaves the transposing PV reads with 2-way bank
+// conflicts (each half wave's 8 keys x 2 chunks fall in 8 slots); this map,
+// found by timing all 20,160 linear maps on gfx950 with this kernel's two read
+// patterns, serves those reads at 1.8x the rate and the QK^T b128 reads at the
+// rate of the plain swizzle. 0 selects the plain one.
+#ifndef RD4_PF_SWZ
+#define RD4_PF_SWZ 1
+#endif
+__device__ __forceinline__ int swz(int r) {
+  if (!RD4_PF_SWZ) return r & 15;
+  return ((r & 1) ? 8 : 0) ^ ((r & 2) ? 7 : 0) ^ ((r & 4) ? 2 : 0) ^ ((r & 8) ? 4 : 0);
 }
 
 }  // namespace
@@ -221,63 +272,53 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   for (int r = 0; r < ND; ++r) {
     const int c = (w * ND + r) * 64 + lane;
     const int key = c >> 5, slot = c & 31;
-    k_goff[r] = (uint32_t)(key * (int)kvstride + 16 * (slot ^ (key & 15)));
+    k_goff[r] = (uint32_t)(key * (int)kvstride + 16 * (slot ^ swz(key)));
   }
-  auto issue_k = [&](int blk, int stage) {
-    uint8_t *kd = smem + stage * kKBytes;
+  // The block's first key as a uniform (scalar) address and each lane's chunk
+  // as a 32-bit offset from it: the DMA then takes the saddr + voffset form and
+  // the loop keeps no 64-bit per-lane pointers.
+  auto uniform_ptr = [](const uint8_t *ptr) {
+    const uint64_t a = (uint64_t)ptr;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return (const uint8_t *)(((uint64_t)hi << 32) | lo);
+  };
+  auto issue_kv = [&](const uint8_t *base, uint8_t *dst, int blk) {
     const int j0 = blk * kBN;
-    const uint8_t *src = kbase + (int64_t)j0 * kvstride;
+    const uint8_t *src = uniform_ptr(base + (int64_t)j0 * kvstride);
     if (j0 + kBN - 1 <= kend) {
 #pragma unroll
-      for (int r = 0; r < ND; ++r)
-        __builtin_amdgcn_global_load_lds((const void *)(src + k_goff[r]),
-                                         (lds_void *)(kd + (w * ND + r) * 1024), 16, 0, 0);
+      for (int r = 0; r < ND; ++r) {
+        uint32_t off = k_goff[r];
+        __asm__("" : "+v"(off));  // keeps the offset 32-bit (no hoisted 64-bit copy)
+        __builtin_amdgcn_global_load_lds((const void *)(src + off), (lds_void *)(dst + (w * ND + r) * 1024), 16, 0, 0);
+      }
     } else {  // last block: keys past kend re-read a valid row (masked later)
 #pragma unroll
       for (int r = 0; r < ND; ++r) {
         const int c = (w * ND + r) * 64 + lane;
         const int key = c >> 5, slot = c & 31;
-        const int jk = min(j0 + key, kend);
+        const int jk = min(key, kend - j0);
         __builtin_amdgcn_global_load_lds(
-            (const void *)(kbase + (int64_t)jk * kvstride + 16 * (slot ^ (key & 15))),
-            (lds_void *)(kd + (w * ND + r) * 1024), 16, 0, 0);
+            (const void *)(src + (uint32_t)(jk * (int)kvstride + 16 * (slot ^ swz(key)))),
+            (lds_void *)(dst + (w * ND + r) * 1024), 16, 0, 0);
       }
     }
   };
+  auto issue_k = [&](int blk, int stage) { issue_kv(kbase, smem + stage * kKBytes, blk); };
   // V: same DMA and swizzle as K, into its own stages.
-  auto issue_v = [&](int blk, int stage) {
-    uint8_t *vd = smem + (kKStages + stage) * kKBytes;
-    const int j0 = blk * kBN;
-    const uint8_t *src = vbase + (int64_t)j0 * kvstride;
-    if (j0 + kBN - 1 <= kend) {
-#pragma unroll
-      for (int r = 0; r < ND; ++r)
-        __builtin_amdgcn_global_load_lds((const void *)(src + k_goff[r]),
-                                         (lds_void *)(vd + (w * ND + r) * 1024), 16, 0, 0);
-    } else {
-#pragma unroll
-      for (int r = 0; r < ND; ++r) {
-        const int c = (w * ND + r) * 64 + lane;
-        const int key = c >> 5, slot = c & 31;
-        const int jk = min(j0 + key, kend);
-        __builtin_amdgcn_global_load_lds(
-            (const void *)(vbase + (int64_t)jk * kvstride + 16 * (slot ^ (key & 15))),
-            (lds_void *)(vd + (w * ND + r) * 1024), 16, 0, 0);
-      }
-    }
-  };
+  auto issue_v = [&](int blk, int stage) { issue_kv(vbase, smem + (kKStages + stage) * kKBytes, blk); };
   // PV operand by transposing load: in each 16-lane group, source lane s points
   // at key (base + s/4), dims 4(s%4)..+3 of a 16-dim tile; lane r then receives
   // dim r of those 4 keys. Key bits 0-3 select the swizzle (base is a multiple
   // of 16 apart from the lane group's 4g), so the per-lane part is fixed.
   const int tr_kx = 4 * g + (n >> 2);                       // key & 15 of this source lane
   const int tr_off = tr_kx * (kHD * 2) + 8 * (n & 1);        // row and 8-byte half
-  const int tr_m = 16 * ((n >> 1 & 1) ^ tr_kx);             // swizzle term of the chunk
+  const int tr_m = 16 * ((n >> 1 & 1) ^ swz(tr_kx));        // swizzle term of the chunk
   // LDS read offsets of the MFMA operands (block-invariant).
   // K: key 16kt + n, dims 32b + 8g: slot (4b + g) ^ n = 4(b ^ (n>>2)) + (g ^ (n&3)).
   int k_loff[8];
 #pragma unroll
-  for (int b = 0; b < 8; ++b) k_loff[b] = n * (kHD * 2) + 64 * (b ^ (n >> 2)) + 16 * (g ^ (n & 3));
+  for (int b = 0; b < 8; ++b) k_loff[b] = n * (kHD * 2) + 16 * ((4 * b + g) ^ swz(n));
 
   // Issue order: K0 V0 K1, then in block j: V(j+1), K(j+2). At the top of block
   // j the loads issued after V(j) are K(j+1)'s only, so waiting until at most
@@ -322,27 +363,64 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       for (int kt = 0; kt < 4; ++kt) s[sl][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
     // fragment f = 8*kt + b of the block: key tile kt, 32-dim step b; a ring of
     // 2 x 4 fragments keeps the next four reads in flight behind four MFMA pairs
-    u32x4 kb[2][4];
+    // step h covers fragments f = kQG*h .. +kQG-1 (key tile f / 8, 32-dim step
+    // f % 8); a ring of kQD steps keeps kQD - 1 steps of reads in flight
+    constexpr int kSteps = 32 / kQG;
+    u32x4 kb[kQD][kQG];
+    pf_prio<2>(w);
+    auto read_kb = [&](int buf, int h) {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) kb[0][b] = (RD4_PF_KNOB & 1) ? __builtin_bit_cast(u32x4, qf[0][b]) : *(const u32x4 *)(kd + k_loff[b]);
-#pragma unroll
-    for (int h = 0; h < 8; ++h) {  // half-tile h: kt = h/2, b = 4*(h&1) .. +3
-      if (h < 7) {
-        const int kt1 = (h + 1) >> 1, b1 = 4 * ((h + 1) & 1);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          kb[(h + 1) & 1][b] = (RD4_PF_KNOB & 1) ? __builtin_bit_cast(u32x4, qf[0][(b + h) & 7]) : *(const u32x4 *)(kd + kt1 * 16 * (kHD * 2) + k_loff[b1 + b]);
+      for (int b = 0; b < kQG; ++b) {
+        const int f = kQG * h + b;
+        kb[buf][b] = (RD4_PF_KNOB & 1) ? __builtin_bit_cast(u32x4, qf[0][(f + h) & 7])
+                                       : *(const u32x4 *)(kd + (f >> 3) * 16 * (kHD * 2) + k_loff[f & 7]);
       }
-      const int kt = h >> 1, b0 = 4 * (h & 1);
+    };
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const half8 kf = __builtin_bit_cast(half8, kb[h & 1][b]);
+    for (int h = 0; h < kQD - 1; ++h) read_kb(h, h);
+#pragma unroll
+    for (int h = 0; h < kSteps; ++h) {
+      if (h + kQD - 1 < kSteps) read_kb((h + kQD - 1) % kQD, h + kQD - 1);
+#pragma unroll
+      for (int b = 0; b < kQG; ++b) {
+        const int f = kQG * h + b, kt = f >> 3;
+        const half8 kf = __builtin_bit_cast(half8, kb[h % kQD][b]);
 #pragma unroll
         for (int sl = 0; sl < NSL; ++sl)
           s[sl][kt] = (RD4_PF_KNOB & 32) ? s[sl][kt] + (float)kf[0]
-                      : __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][b0 + b], s[sl][kt], 0, 0, 0);
+                      : __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][f & 7], s[sl][kt], 0, 0, 0);
       }
+      if (RD4_PF_SB & 4) {  // within the step: one read, one MFMA, in turn
+#pragma unroll
+        for (int b = 0; b < kQG; ++b) {
+          if (h + kQD - 1 < kSteps) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, NSL, 0);
+        }
+      }
+      if (RD4_PF_SB & 1) __builtin_amdgcn_sched_barrier(0);
     }
+    half8 vb[kPVD][2];
+    // step t: key group kg = t / 8, dim tiles 2(t % 8), +1
+    auto read_vb = [&](int buf, int t) {
+      const int kg = t >> 3, dt0 = 2 * (t & 7);
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const uint8_t *a0 = vd + (32 * kg) * (kHD * 2) + tr_off + ((32 * (dt0 + d)) ^ tr_m);
+        if (RD4_PF_KNOB & 2) {
+          vb[buf][d] = qf[0][(dt0 + d) & 7];
+          continue;
+        }
+        const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4 *)a0);
+        const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4 *)(a0 + 16 * (kHD * 2)));
+        vb[buf][d] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    };
+    if (RD4_PF_VEARLY) {  // the first PV operands do not depend on the softmax
+#pragma unroll
+      for (int t = 0; t < kPVD - 1; ++t) read_vb(t, t);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    pf_prio<0>(w);
     // ---- online softmax per slab: lane = row n, keys 16kt + 4g + i
     half8 pf[NSL][2];
     if (RD4_PF_KNOB & 4) {
@@ -354,15 +432,21 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
 #pragma unroll
     for (int sl = 0; sl < NSL; ++sl) {
       float tmax = -INFINITY;
+      if (!RD4_PF_MASKBR || need_mask) {  // wave-uniform: most blocks skip the per-element compares
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = s[sl][kt][i];
-          if (need_mask && j0 + 16 * kt + 4 * g + i > lim_row[sl]) v = -INFINITY;
-          s[sl][kt][i] = v;
-          tmax = fmaxf(tmax, v);
-        }
+          for (int i = 0; i < 4; ++i)
+            if ((RD4_PF_MASKBR || need_mask) && j0 + 16 * kt + 4 * g + i > lim_row[sl]) s[sl][kt][i] = -INFINITY;
+      }
+      // max and sum as trees (depth 4, not a 16-long dependent chain)
+      {
+        float m4[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          m4[kt] = fmaxf(fmaxf(s[sl][kt][0], s[sl][kt][1]), fmaxf(s[sl][kt][2], s[sl][kt][3]));
+        tmax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+      }
       tmax = max_groups4(tmax);
       // The reference max only moves when the block max exceeds it by more than
       // 2^8 (p <= 256 stays exact enough in f16 and l, O are f32): most blocks
@@ -377,16 +461,14 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
         m_run[sl] = m_new;
       }
       const float m_use = (m_run[sl] == -INFINITY) ? 0.0f : m_run[sl];
-      float psum = 0.0f;
+      float ps4[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = __builtin_amdgcn_exp2f(s[sl][kt][i] - m_use);
-          s[sl][kt][i] = e;
-          psum += e;
-        }
-      l_run[sl] += psum;
+        for (int i = 0; i < 4; ++i) s[sl][kt][i] = __builtin_amdgcn_exp2f(s[sl][kt][i] - m_use);
+        ps4[kt] = (s[sl][kt][0] + s[sl][kt][1]) + (s[sl][kt][2] + s[sl][kt][3]);
+      }
+      l_run[sl] += (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
       // B operand of PV: k-slot 8h + i <-> key 32*kg + 16*(i>>2) + 4h + (i&3)
 #pragma unroll
       for (int kg = 0; kg < 2; ++kg)
@@ -396,36 +478,26 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
     // ---- O^T += V^T P^T: A = 16 dims x 32 keys of V (k-slot 8g + j is key
     // 32kg + 16(j/4) + 4g + j%4, as in pf), two transposing loads per operand;
     // the next two dim tiles' operands are read while the current ones run.
+    pf_prio<2>(w);
+    if (!RD4_PF_VEARLY) {
 #pragma unroll
-    for (int kg = 0; kg < 2; ++kg) {
-      half8 vb[2][2];
-      auto read_vb = [&](int buf, int dt0) {
-#pragma unroll
-        for (int d = 0; d < 2; ++d) {
-          const uint8_t *a0 = vd + (32 * kg) * (kHD * 2) + tr_off + ((32 * (dt0 + d)) ^ tr_m);
-          if (RD4_PF_KNOB & 2) {
-            vb[buf][d] = qf[0][(dt0 + d) & 7];
-            continue;
-          }
-          const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4 *)a0);
-          const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4 *)(a0 + 16 * (kHD * 2)));
-          vb[buf][d] = __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        }
-      };
-      read_vb(0, 0);
-#pragma unroll
-      for (int q2 = 0; q2 < 8; ++q2) {
-        if (q2 < 7) read_vb((q2 + 1) & 1, 2 * (q2 + 1));
-#pragma unroll
-        for (int d = 0; d < 2; ++d) {
-          const int dt = 2 * q2 + d;
-#pragma unroll
-          for (int sl = 0; sl < NSL; ++sl)
-            o[sl][dt] = (RD4_PF_KNOB & 32) ? o[sl][dt] + (float)vb[q2 & 1][d][0]
-                        : __builtin_amdgcn_mfma_f32_16x16x32_f16(vb[q2 & 1][d], pf[sl][kg], o[sl][dt], 0, 0, 0);
-        }
-      }
+      for (int t = 0; t < kPVD - 1; ++t) read_vb(t, t);
     }
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      if (t + kPVD - 1 < 16) read_vb((t + kPVD - 1) % kPVD, t + kPVD - 1);
+      const int kg = t >> 3;
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int dt = 2 * (t & 7) + d;
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl)
+          o[sl][dt] = (RD4_PF_KNOB & 32) ? o[sl][dt] + (float)vb[t % kPVD][d][0]
+                      : __builtin_amdgcn_mfma_f32_16x16x32_f16(vb[t % kPVD][d], pf[sl][kg], o[sl][dt], 0, 0, 0);
+      }
+      if (RD4_PF_SB & 2) __builtin_amdgcn_sched_barrier(0);
+    }
+    pf_prio<0>(w);
   }
 
   // ---- epilogue: l over the 4 key groups, normalize, gate, store
