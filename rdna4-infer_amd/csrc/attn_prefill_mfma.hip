@@ -9,23 +9,26 @@
 //
 // Work decomposition: the (query, head) pairs of one kv head form rows
 // r = query * group + head_in_group, so every head of a GQA group shares the K/V
-// tiles. CTA = 8 waves = 128 consecutive rows of one kv head; each wave owns 16
-// rows (one MFMA slab), two waves per SIMD so one wave's softmax overlaps
-// another's MFMAs. The CTA walks 64-key blocks:
-//   * K block (64 x 256 f16) arrives by global->LDS DMA, row-major with the
-//     16-byte chunks of row r XOR-swizzled by r & 15 (conflict-free reads);
+// tiles. Default CTA = 12 waves = 192 consecutive rows of one kv head; each wave
+// owns 16 rows (one MFMA slab), three waves per SIMD so one wave's softmax and
+// LDS waits overlap the others' MFMAs. The CTA walks 64-key blocks:
+//   * K block (64 x 256 f16) arrives by global->LDS DMA (scalar base + 32-bit
+//     lane offsets), row-major with the 16-byte chunks of key r permuted by
+//     swz(r) (conflict-free for both read patterns below);
 //   * V block arrives the same way, same swizzle; the PV operand (16 dims x
 //     8 keys per lane group) is read straight out of it with the gfx950
 //     transposing LDS load (ds_read_b64_tr_b16), so no transpose pass;
-//   block j+1's DMA is in flight while block j computes (K and V
-//   double-buffered, one CTA barrier per block);
-//   within a block, the next MFMA operand fragments are read from LDS while
-//   the current ones feed the MFMAs.
+//   three K stages and two V stages: K two blocks ahead, V one, one CTA
+//   barrier per block;
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_f16 (A = 16 keys x 32 dims of K from
-//     LDS, reused by both slabs; B = the wave's query rows in registers);
+//     LDS, B = the wave's query rows in registers), O^T += V^T P^T likewise;
+//     in both phases a ring of operand fragments keeps several steps of LDS
+//     reads in flight ahead of their MFMAs, and scheduling fences hold the
+//     compiler to that order;
 //   * online softmax in registers (exp2 domain, lazy O rescale); the C layout
 //     of S^T is the B operand of O^T += V^T P^T, so p never leaves registers;
-//   * causal masking is applied only in blocks that cross a row's limit.
+//   * causal masking only in blocks that cross a row's limit (a wave-uniform
+//     branch).
 // Row blocks are scheduled heaviest (latest queries) first.
 #include <cstdlib>
 
@@ -45,7 +48,6 @@ typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
 
 constexpr int kHD = 256;
-constexpr int kBM = 128;                   // rows per CTA
 constexpr int kBN = 64;                    // keys per block
 constexpr int kKBytes = kBN * kHD * 2;     // K block, 32 KiB
 // LDS: three K stages then two V stages (the whole 160 KiB): K streams two
@@ -64,7 +66,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 #ifndef RD4_PF_PVD
 #define RD4_PF_PVD 3
 #endif
-constexpr int kPVD = RD4_PF_PVD;
+constexpr int kPVD0 = RD4_PF_PVD;
 // QK^T operand ring: kQD steps of kQG K fragments
 #ifndef RD4_PF_QKG
 #define RD4_PF_QKG 2
@@ -72,7 +74,14 @@ constexpr int kPVD = RD4_PF_PVD;
 #ifndef RD4_PF_QKD
 #define RD4_PF_QKD 4
 #endif
-constexpr int kQG = RD4_PF_QKG, kQD = RD4_PF_QKD;
+constexpr int kQG = RD4_PF_QKG, kQD0 = RD4_PF_QKD;
+// the same at three waves per SIMD (12 waves per CTA)
+#ifndef RD4_PF_QKD_W12
+#define RD4_PF_QKD_W12 3
+#endif
+#ifndef RD4_PF_PVD_W12
+#define RD4_PF_PVD_W12 3
+#endif
 // scheduling fences (experiment): 1 after each QK^T step, 2 after each PV step,
 // so the operand reads stay as far ahead of their MFMAs as written
 #ifndef RD4_PF_SB
@@ -85,6 +94,9 @@ constexpr int kQG = RD4_PF_QKG, kQD = RD4_PF_QKD;
 // causal mask under a wave-uniform branch (1) or applied to every block (0)
 #ifndef RD4_PF_MASKBR
 #define RD4_PF_MASKBR 1
+#endif
+#ifndef RD4_PF_DMAPOS
+#define RD4_PF_DMAPOS 1
 #endif
 #ifndef RD4_PF_PRIO
 #define RD4_PF_PRIO 0
@@ -127,12 +139,19 @@ __device__ __forceinline__ int swz(int r) {
 
 }  // namespace
 
-// W waves of NSL 16-row slabs each (W * 16 * NSL = 128 rows per CTA).
+// W waves of NSL 16-row slabs each (W * 16 * NSL rows per CTA).
 template <int W, int NSL>
 __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) {
   constexpr int kRowsWT = 16 * NSL;         // rows per wave
-  constexpr int ND = 2048 / (64 * W);       // 16-byte DMA chunks per lane per K (or V) block
-  static_assert(W * kRowsWT == kBM, "a CTA holds 128 rows");
+  // a K (or V) block is 32 wave-chunks of 64 x 16 bytes; wave w takes chunks
+  // w*ND .. w*ND+ND-1 below 32 (nk of them)
+  constexpr int ND = (32 + W - 1) / W;
+  constexpr bool kEven = 32 % W == 0;
+  constexpr int kBM = W * kRowsWT;          // rows per CTA
+  // ring depths in steps: with two slabs every step feeds twice the MFMAs
+  // (and with three waves per SIMD the registers allow shorter rings only)
+  constexpr int kQD = NSL > 1 ? 2 : W > 8 ? RD4_PF_QKD_W12 : kQD0;
+  constexpr int kPVD = NSL > 1 ? 2 : W > 8 ? RD4_PF_PVD_W12 : kPVD0;
   extern __shared__ __align__(16) uint8_t smem[];
   // the wave index is uniform: readfirstlane keeps DMA bases and LDS
   // destinations in scalar registers
@@ -270,7 +289,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   uint32_t k_goff[ND];  // byte offset of this lane's chunk r from the block's first key (scalar base + 32-bit vector offset)
 #pragma unroll
   for (int r = 0; r < ND; ++r) {
-    const int c = (w * ND + r) * 64 + lane;
+    const int c = min(w * ND + r, 31) * 64 + lane;
     const int key = c >> 5, slot = c & 31;
     k_goff[r] = (uint32_t)(key * (int)kvstride + 16 * (slot ^ swz(key)));
   }
@@ -288,6 +307,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
     if (j0 + kBN - 1 <= kend) {
 #pragma unroll
       for (int r = 0; r < ND; ++r) {
+        if (!kEven && w * ND + r >= 32) break;
         uint32_t off = k_goff[r];
         __asm__("" : "+v"(off));  // keeps the offset 32-bit (no hoisted 64-bit copy)
         __builtin_amdgcn_global_load_lds((const void *)(src + off), (lds_void *)(dst + (w * ND + r) * 1024), 16, 0, 0);
@@ -295,6 +315,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
     } else {  // last block: keys past kend re-read a valid row (masked later)
 #pragma unroll
       for (int r = 0; r < ND; ++r) {
+        if (!kEven && w * ND + r >= 32) break;
         const int c = (w * ND + r) * 64 + lane;
         const int key = c >> 5, slot = c & 31;
         const int jk = min(key, kend - j0);
@@ -332,8 +353,16 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int vs = blk & 1;
     if (blk + 1 < n_blocks) {
-      // K(j), V(j) landed; K(j+1) (its ND DMA instructions) may fly
-      __builtin_amdgcn_s_waitcnt((ND & 15) | ((ND >> 4) << 14) | (7 << 4) | (15 << 8));
+      // K(j), V(j) landed; K(j+1) (this wave's nk DMA instructions) may fly
+      if (kEven) {
+        __builtin_amdgcn_s_waitcnt((ND & 15) | ((ND >> 4) << 14) | (7 << 4) | (15 << 8));
+      } else {
+        const int nk = min(max(32 - w * ND, 0), ND);
+        if (nk >= 3) __builtin_amdgcn_s_waitcnt(3 | (7 << 4) | (15 << 8));
+        else if (nk == 2) __builtin_amdgcn_s_waitcnt(2 | (7 << 4) | (15 << 8));
+        else if (nk == 1) __builtin_amdgcn_s_waitcnt(1 | (7 << 4) | (15 << 8));
+        else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+      }
     } else {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
@@ -344,9 +373,12 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
 #else
     __syncthreads();
 #endif
+    const int ks2 = ks == 0 ? 2 : ks - 1;  // stage of K(blk + 2): (blk + 2) % 3
+    // DMA issue points (RD4_PF_DMAPOS, default 1): 0 both at the block top, 1 K(blk + 2)
+    // after the QK^T phase, 3 both after it
     if (!(RD4_PF_KNOB & 8)) {
-      if (blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
-      if (blk + 2 < n_blocks) issue_k(blk + 2, ks == 0 ? 2 : ks - 1);  // (blk + 2) % 3
+      if (RD4_PF_DMAPOS != 3 && blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
+      if (RD4_PF_DMAPOS == 0 && blk + 2 < n_blocks) issue_k(blk + 2, ks2);
     }
     const uint8_t *kd = smem + ks * kKBytes;
     const uint8_t *vd = smem + (kKStages + vs) * kKBytes;
@@ -421,6 +453,11 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       __builtin_amdgcn_sched_barrier(0);
     }
     pf_prio<0>(w);
+    if (!(RD4_PF_KNOB & 8) && RD4_PF_DMAPOS != 0) {
+      if (RD4_PF_DMAPOS == 3 && blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
+      if (blk + 2 < n_blocks) issue_k(blk + 2, ks2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // ---- online softmax per slab: lane = row n, keys 16kt + 4g + i
     half8 pf[NSL][2];
     if (RD4_PF_KNOB & 4) {
@@ -537,17 +574,22 @@ bool prefill_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_
 }
 
 hipError_t prefill_mfma_launch(const PrefillArgs &p, hipStream_t st) {
-  const int grp = p.n_head / p.n_head_kv;
-  const int n_rb = (p.n_q * grp + kBM - 1) / kBM;
-  dim3 grid((unsigned)(n_rb * p.n_head_kv));
   static const int shape = [] {
     const char *e = std::getenv("RD4_PREFILL_SHAPE");
     return e ? std::atoi(e) : 0;
   }();
+  const int grp = p.n_head / p.n_head_kv;
+  const int bm = shape == 2 ? 256 : shape == 0 ? 192 : 128;  // rows per CTA
+  const int n_rb = (p.n_q * grp + bm - 1) / bm;
+  dim3 grid((unsigned)(n_rb * p.n_head_kv));
   if (shape == 1)  // 4 waves x 32 rows (one wave per SIMD)
     hipLaunchKernelGGL((prefill_mfma_kernel<4, 2>), grid, dim3(256), (size_t)kLdsBytes, st, p);
-  else  // 8 waves x 16 rows (two waves per SIMD)
+  else if (shape == 2)  // 8 waves x 32 rows (two waves per SIMD)
+    hipLaunchKernelGGL((prefill_mfma_kernel<8, 2>), grid, dim3(512), (size_t)kLdsBytes, st, p);
+  else if (shape == 3)  // 8 waves x 16 rows (two waves per SIMD)
     hipLaunchKernelGGL((prefill_mfma_kernel<8, 1>), grid, dim3(512), (size_t)kLdsBytes, st, p);
+  else  // 12 waves x 16 rows (three waves per SIMD)
+    hipLaunchKernelGGL((prefill_mfma_kernel<12, 1>), grid, dim3(768), (size_t)kLdsBytes, st, p);
   return hipGetLastError();
 }
 
