@@ -46,6 +46,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
+// LDS reads through an address-space-3 pointer: a generic pointer that the
+// compiler later narrows to LDS is counted as a flat access, and its waits
+// then become waits for every outstanding LDS read
+typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
 
 constexpr int kHD = 256;
 constexpr int kBN = 64;                    // keys per block
@@ -335,6 +339,11 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   const int tr_kx = 4 * g + (n >> 2);                       // key & 15 of this source lane
   const int tr_off = tr_kx * (kHD * 2) + 8 * (n & 1);        // row and 8-byte half
   const int tr_m = 16 * ((n >> 1 & 1) ^ swz(tr_kx));        // swizzle term of the chunk
+  // lane offset of dim tile dt for dt = 0..7; tr_m < 256, so tile dt + 8 is
+  // the same offset + 256 (an instruction immediate)
+  int v_loff[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) v_loff[dt] = tr_off + ((32 * dt) ^ tr_m);
   // LDS read offsets of the MFMA operands (block-invariant).
   // K: key 16kt + n, dims 32b + 8g: slot (4b + g) ^ n = 4(b ^ (n>>2)) + (g ^ (n&3)).
   int k_loff[8];
@@ -395,41 +404,30 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       for (int kt = 0; kt < 4; ++kt) s[sl][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
     // fragment f = 8*kt + b of the block: key tile kt, 32-dim step b; a ring of
     // 2 x 4 fragments keeps the next four reads in flight behind four MFMA pairs
-    // step h covers fragments f = kQG*h .. +kQG-1 (key tile f / 8, 32-dim step
-    // f % 8); a ring of kQD steps keeps kQD - 1 steps of reads in flight
-    constexpr int kSteps = 32 / kQG;
-    u32x4 kb[kQD][kQG];
     pf_prio<2>(w);
-    auto read_kb = [&](int buf, int h) {
-#pragma unroll
-      for (int b = 0; b < kQG; ++b) {
-        const int f = kQG * h + b;
-        kb[buf][b] = (RD4_PF_KNOB & 1) ? __builtin_bit_cast(u32x4, qf[0][(f + h) & 7])
-                                       : *(const u32x4 *)(kd + (f >> 3) * 16 * (kHD * 2) + k_loff[f & 7]);
-      }
+    // fragment f (key tile f / 8, 32-dim step f % 8) is read kAhead fragments
+    // before its MFMA, into a ring of kAhead + 1 registers; a scheduling fence
+    // after every read and MFMA keeps that order (the compiler would otherwise
+    // reorder the reads and wait for all of them)
+    constexpr int kAhead = (kQD - 1) * kQG, kRing = kAhead + 1;
+    u32x4 kr[kRing];
+    auto read_kf = [&](int f) {
+      kr[f % kRing] = (RD4_PF_KNOB & 1) ? __builtin_bit_cast(u32x4, qf[0][(f + 1) & 7])
+                                        : *(const lds_u32x4 *)(kd + (f >> 3) * 16 * (kHD * 2) + k_loff[f & 7]);
+      __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
-    for (int h = 0; h < kQD - 1; ++h) read_kb(h, h);
+    for (int f = 0; f < kAhead; ++f) read_kf(f);
 #pragma unroll
-    for (int h = 0; h < kSteps; ++h) {
-      if (h + kQD - 1 < kSteps) read_kb((h + kQD - 1) % kQD, h + kQD - 1);
+    for (int f = 0; f < 32; ++f) {
+      if (f + kAhead < 32) read_kf(f + kAhead);
+      const int kt = f >> 3;
+      const half8 kf = __builtin_bit_cast(half8, kr[f % kRing]);
 #pragma unroll
-      for (int b = 0; b < kQG; ++b) {
-        const int f = kQG * h + b, kt = f >> 3;
-        const half8 kf = __builtin_bit_cast(half8, kb[h % kQD][b]);
-#pragma unroll
-        for (int sl = 0; sl < NSL; ++sl)
-          s[sl][kt] = (RD4_PF_KNOB & 32) ? s[sl][kt] + (float)kf[0]
-                      : __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][f & 7], s[sl][kt], 0, 0, 0);
-      }
-      if (RD4_PF_SB & 4) {  // within the step: one read, one MFMA, in turn
-#pragma unroll
-        for (int b = 0; b < kQG; ++b) {
-          if (h + kQD - 1 < kSteps) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, NSL, 0);
-        }
-      }
-      if (RD4_PF_SB & 1) __builtin_amdgcn_sched_barrier(0);
+      for (int sl = 0; sl < NSL; ++sl)
+        s[sl][kt] = (RD4_PF_KNOB & 32) ? s[sl][kt] + (float)kf[0]
+                    : __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][f & 7], s[sl][kt], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
     half8 vb[kPVD][2];
     // step t: key group kg = t / 8, dim tiles 2(t % 8), +1
@@ -437,7 +435,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       const int kg = t >> 3, dt0 = 2 * (t & 7);
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
-        const uint8_t *a0 = vd + (32 * kg) * (kHD * 2) + tr_off + ((32 * (dt0 + d)) ^ tr_m);
+        const uint8_t *a0 = vd + v_loff[(dt0 + d) & 7] + (32 * kg) * (kHD * 2) + 256 * ((dt0 + d) >> 3);
         if (RD4_PF_KNOB & 2) {
           vb[buf][d] = qf[0][(dt0 + d) & 7];
           continue;
