@@ -143,30 +143,6 @@ __device__ __forceinline__ uint32_t i8x2_to_h2(uint32_t v) {
   x = x + c;
   return __builtin_bit_cast(uint32_t, x);
 }
-#ifndef RD4_SDWA_V
-#define RD4_SDWA_V 0
-#endif
-constexpr bool kSdwaV = RD4_SDWA_V != 0;
-// The f16 MFMA operands of four keys' 2-dim int8 words u0..u3: r[0] = {u0.b0,
-// u1.b0}, r[1] = {u2.b0, u3.b0}, r[2] = {u0.b1, u1.b1}, r[3] = {u2.b1, u3.b1},
-// each half a sign-extended byte converted by one SDWA op (the first of a pair
-// zeroes the high half, the second keeps the low one). The closing s_nop gives
-// the last results the two wait states a VALU write needs before an MFMA reads
-// it as a source operand; the compiler does not see inside the block.
-__device__ __forceinline__ void sdwa_i8_quad(const uint32_t *u, uint32_t *r) {
-  __asm__(
-      "v_cvt_f16_i16_sdwa %0, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-      "v_cvt_f16_i16_sdwa %1, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-      "v_cvt_f16_i16_sdwa %2, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-      "v_cvt_f16_i16_sdwa %3, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-      "v_cvt_f16_i16_sdwa %0, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
-      "v_cvt_f16_i16_sdwa %1, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
-      "v_cvt_f16_i16_sdwa %2, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
-      "v_cvt_f16_i16_sdwa %3, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
-      "s_nop 1"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-      : "v"(u[0]), "v"(u[1]), "v"(u[2]), "v"(u[3]));
-}
 // Two 4-bit values (bits 0-3 and 16-19 of v) -> two f16 of (n - 8).
 __device__ __forceinline__ uint32_t nib2_to_h2(uint32_t v) {
   const uint32_t w = (v & 0x000f000fu) | 0x64006400u;  // 1024 + n
@@ -1314,8 +1290,6 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         const uint32_t w01_0 = __builtin_amdgcn_perm(u[1], u[0], 0x0c040c00u);
         const uint32_t w23_0 = __builtin_amdgcn_perm(u[3], u[2], 0x0c040c00u);
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        uint32_t sq[4];
-        if constexpr (VT == Q8_0 && kSdwaV) sdwa_i8_quad(u, sq);
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           uint32_t a01, a23;
@@ -1324,9 +1298,6 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
             const h2 c = {(_Float16)-1040.0f, (_Float16)-1040.0f};  // 1024 + 16
             a01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[1], u[0], sel) | 0x64006400u) + c);
             a23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(u[3], u[2], sel) | 0x64006400u) + c);
-          } else if constexpr (VT == Q8_0 && kSdwaV) {
-            a01 = sq[2 * e];
-            a23 = sq[2 * e + 1];
           } else if constexpr (VT == Q8_0) {
             const uint32_t sel = e ? 0x0c050c01u : 0x0c040c00u;
             const h2 c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
