@@ -167,8 +167,8 @@ def test_prefill_append_config5_full(rd4, orc, dev, monkeypatch):
     queries at 4096..8191 over 8192 f16 keys, causal, gated, the chunk's K/V rows
     appended as q8_0), at full size (graph.cuh:1462 store + 1479-1535):
     - all 4096 x 24 output rows against the generic (VALU) kernel on the same inputs;
-    - the first and last query row of every eighth 128-row CTA block, plus the
-      chunk's first and last rows, against the f64 oracle;
+    - the first and last query row of every eighth 192-row (and 128-row) CTA
+      block, plus the chunk's first and last rows, against the f64 oracle;
     - the 4096 appended q8_0 rows of each cache byte-for-byte against the oracle's
       quantization of the same f32 rows."""
     import torch
@@ -204,13 +204,57 @@ def test_prefill_append_config5_full(rd4, orc, dev, monkeypatch):
     torch.cuda.synchronize()
     check_close(got.ravel(), ref.cpu().numpy().ravel(), "config 5 mfma vs generic, all rows")
     assert np.array_equal(sig, gd2.cpu().numpy())
-    # CTA-boundary rows against the oracle: a CTA holds 128 (query, head) rows
+    # CTA-boundary rows against the oracle: a CTA holds 192 (query, head) rows
+    # (12 waves of 16; 128 in the 8-wave shape)
     grp = nh // nkv
-    blocks = range(0, (nq * grp + 127) // 128, 8)
-    rows = sorted({0, nq - 1} | {min(nq - 1, 128 * c // grp) for c in blocks} |
-                  {min(nq - 1, (128 * c + 127) // grp) for c in blocks})
+    rows = {0, nq - 1}
+    for bm in (192, 128):
+        blocks = range(0, (nq * grp + bm - 1) // bm, 8)
+        rows |= {min(nq - 1, bm * c // grp) for c in blocks} | {min(nq - 1, (bm * c + bm - 1) // grp) for c in blocks}
+    rows = sorted(rows)
     rows = np.int32(rows)
     want = orc.attn_batch(q[rows].astype(np.float32), k, v, pos0 + rows, nh, nkv, hd, 1 / 16, 1, 1,
                           threads=8)
     _, want = orc.sigmoid_gate(g[rows], want)
     check_close(got[rows].ravel(), want, "config 5 rows vs oracle (%d rows)" % len(rows))
+
+
+@pytest.mark.parametrize("shape", ["1", "2", "3"])
+def test_prefill_shape_variants(shape):
+    """The kernel's other CTA shapes (RD4_PREFILL_SHAPE: 1 = 4 waves x 32 rows,
+    2 = 8 waves x 32 rows, 3 = 8 waves x 16 rows; the default is 12 x 16) on a
+    GQA chunk with a masked last block, against the f64 oracle on every query
+    row. Run in a child process, since the library reads the variable once."""
+    import os
+    import subprocess
+    import sys
+    code = r'''
+import sys
+sys.path.insert(0, "tests"); sys.path.insert(0, "oracle")
+import numpy as np, torch
+from conftest import load_package
+import oracle as orc
+from gpu_util import to_dev, check_close
+rd4 = load_package(); dev = torch.device("cuda:0")
+nh, nkv, hd, pos0, nq = 24, 4, 256, 333, 301
+n = pos0 + nq
+k = orc.store_rows(1, orc.randn(n * nkv * hd, 41))
+v = orc.store_rows(1, orc.randn(n * nkv * hd, 42))
+q = orc.randn(nq * nh * hd, 43).reshape(nq, nh, hd).astype(np.float16)
+g = orc.randn(nq * nh * hd, 44).reshape(nq, nh, hd)
+out = torch.empty((nq, nh, hd), dtype=torch.float32, device=dev)
+gd = to_dev(g, torch, dev)
+rd4.prefill(to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev), out, pos0, nh, nkv, hd,
+            1 / 16, 1, 1, gate=gd)
+torch.cuda.synchronize()
+rows = np.arange(nq, dtype=np.int32)
+want = orc.attn_batch(q.astype(np.float32), k, v, pos0 + rows, nh, nkv, hd, 1 / 16, 1, 1, threads=8)
+_, want = orc.sigmoid_gate(g, want)
+check_close(out.cpu().numpy().ravel(), want, "shape " + sys.argv[1])
+print("ok")
+'''
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, RD4_PREFILL_SHAPE=shape)
+    r = subprocess.run([sys.executable, "-c", code, shape], cwd=root, env=env, capture_output=True,
+                       text=True, timeout=180)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
