@@ -102,6 +102,13 @@ constexpr int kQG = RD4_PF_QKG, kQD0 = RD4_PF_QKD;
 #ifndef RD4_PF_DMAPOS
 #define RD4_PF_DMAPOS 1
 #endif
+// block max by max3 asm (1) or by fmaxf (0)
+#ifndef RD4_PF_SM
+#define RD4_PF_SM 1
+#endif
+#ifndef RD4_PF_PROBE
+#define RD4_PF_PROBE 0
+#endif
 #ifndef RD4_PF_PRIO
 #define RD4_PF_PRIO 0
 #endif
@@ -139,6 +146,25 @@ __device__ __forceinline__ float max_groups4(float x) {
 __device__ __forceinline__ int swz(int r) {
   if (!RD4_PF_SWZ) return r & 15;
   return ((r & 1) ? 8 : 0) ^ ((r & 2) ? 7 : 0) ^ ((r & 4) ? 2 : 0) ^ ((r & 8) ? 4 : 0);
+}
+
+// max3 and the group max without the compiler's canonicalizing maxes (the
+// operands are finite or -inf, never NaN)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max_groups4_raw(float x) {
+  float a = x, b = x;
+  __asm__("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  float c;
+  __asm__("v_max_f32 %0, %1, %2" : "=v"(c) : "v"(a), "v"(b));
+  float d = c;
+  __asm__("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
+  float r;
+  __asm__("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(c), "v"(d));
+  return r;
 }
 
 }  // namespace
@@ -359,6 +385,11 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   }
   if (n_blocks > 1) issue_k(1, 1);
   int ks = 0;  // K stage of the current block (blk % 3)
+#if RD4_PF_PROBE
+  float pr_a = 0.f, pr_b = 1.f;
+  floatx4 pr_c = {0.f, 0.f, 0.f, 0.f};
+  u32x4 pr_d = {0, 0, 0, 0};
+#endif
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int vs = blk & 1;
     if (blk + 1 < n_blocks) {
@@ -474,15 +505,24 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
           for (int i = 0; i < 4; ++i)
             if ((RD4_PF_MASKBR || need_mask) && j0 + 16 * kt + 4 * g + i > lim_row[sl]) s[sl][kt][i] = -INFINITY;
       }
-      // max and sum as trees (depth 4, not a 16-long dependent chain)
-      {
+      // block max as a tree (max3 in asm: the compiler's fmaxf adds a
+      // canonicalizing max per operand)
+      if (RD4_PF_SM & 1) {
+        const float a0 = max3f(s[sl][0][0], s[sl][0][1], s[sl][0][2]);
+        const float a1 = max3f(s[sl][0][3], s[sl][1][0], s[sl][1][1]);
+        const float a2 = max3f(s[sl][1][2], s[sl][1][3], s[sl][2][0]);
+        const float a3 = max3f(s[sl][2][1], s[sl][2][2], s[sl][2][3]);
+        const float a4 = max3f(s[sl][3][0], s[sl][3][1], s[sl][3][2]);
+        tmax = max3f(max3f(a0, a1, a2), a3, max3f(a4, s[sl][3][3], s[sl][3][3]));
+        tmax = max_groups4_raw(tmax);
+      } else {
         float m4[4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
           m4[kt] = fmaxf(fmaxf(s[sl][kt][0], s[sl][kt][1]), fmaxf(s[sl][kt][2], s[sl][kt][3]));
         tmax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+        tmax = max_groups4(tmax);
       }
-      tmax = max_groups4(tmax);
       // The reference max only moves when the block max exceeds it by more than
       // 2^8 (p <= 256 stays exact enough in f16 and l, O are f32): most blocks
       // then skip the O rescale.
@@ -533,7 +573,19 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       if (RD4_PF_SB & 2) __builtin_amdgcn_sched_barrier(0);
     }
     pf_prio<0>(w);
+#if RD4_PF_PROBE
+    // sensitivity probes (diagnostic builds only): extra independent work per block
+    if (RD4_PF_PROBE & 1)
+      __asm__ volatile(".rept 16\n\tv_add_f32 %0, %0, %2\n\tv_add_f32 %1, %1, %2\n\t.endr" : "+v"(pr_a), "+v"(pr_b) : "v"(sl2));
+    if (RD4_PF_PROBE & 2)
+      __asm__ volatile(".rept 16\n\tv_mfma_f32_16x16x32_f16 %0, %1, %2, %0\n\t.endr\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(pr_c) : "v"(qf[0][0]), "v"(qf[0][1]));
+    if (RD4_PF_PROBE & 4)
+      __asm__ volatile(".rept 16\n\tds_read_b128 %0, %1\n\t.endr\n\ts_waitcnt lgkmcnt(0)" : "=v"(pr_d) : "v"((uint32_t)(uintptr_t)smem + k_loff[0]));
+#endif
   }
+#if RD4_PF_PROBE
+  if (p.scale == 12345.0f) p.out[tid] = pr_a + pr_b + pr_c[0] + (float)pr_d[0];
+#endif
 
   // ---- epilogue: l over the 4 key groups, normalize, gate, store
 #pragma unroll
