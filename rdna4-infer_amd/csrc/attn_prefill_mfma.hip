@@ -86,10 +86,10 @@ constexpr int kQG = RD4_PF_QKG, kQD0 = RD4_PF_QKD;
 #ifndef RD4_PF_PVD_W12
 #define RD4_PF_PVD_W12 3
 #endif
-// scheduling fences (experiment): 1 after each QK^T step, 2 after each PV step,
-// so the operand reads stay as far ahead of their MFMAs as written
+// a scheduling fence after each PV step (2), so the operand reads stay as far
+// ahead of their MFMAs as written (the QK^T reads are always fenced)
 #ifndef RD4_PF_SB
-#define RD4_PF_SB 7
+#define RD4_PF_SB 2
 #endif
 // the first PV operand reads go out before the softmax (1) or after it (0)
 #ifndef RD4_PF_VEARLY
@@ -99,6 +99,8 @@ constexpr int kQG = RD4_PF_QKG, kQD0 = RD4_PF_QKD;
 #ifndef RD4_PF_MASKBR
 #define RD4_PF_MASKBR 1
 #endif
+// where K(j + 2) is requested (0 at the top of block j, 1 after its QK^T phase,
+// 3 with V(j + 1) after it too)
 #ifndef RD4_PF_DMAPOS
 #define RD4_PF_DMAPOS 1
 #endif
@@ -109,15 +111,6 @@ constexpr int kQG = RD4_PF_QKG, kQD0 = RD4_PF_QKD;
 #ifndef RD4_PF_PROBE
 #define RD4_PF_PROBE 0
 #endif
-#ifndef RD4_PF_PRIO
-#define RD4_PF_PRIO 0
-#endif
-// wave priority around the MFMA phases (experiment): 1 raises it for the QK^T and
-// PV phases of every wave, 2 only for the first wave of each SIMD
-template <int V>
-__device__ __forceinline__ void pf_prio(int w) {
-  if (RD4_PF_PRIO == 1 || (RD4_PF_PRIO == 2 && w < 4)) __builtin_amdgcn_s_setprio(V);
-}
 
 __device__ __forceinline__ _Float16 h16(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
@@ -433,9 +426,6 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
     for (int sl = 0; sl < NSL; ++sl)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) s[sl][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    // fragment f = 8*kt + b of the block: key tile kt, 32-dim step b; a ring of
-    // 2 x 4 fragments keeps the next four reads in flight behind four MFMA pairs
-    pf_prio<2>(w);
     // fragment f (key tile f / 8, 32-dim step f % 8) is read kAhead fragments
     // before its MFMA, into a ring of kAhead + 1 registers; a scheduling fence
     // after every read and MFMA keeps that order (the compiler would otherwise
@@ -481,7 +471,6 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       for (int t = 0; t < kPVD - 1; ++t) read_vb(t, t);
       __builtin_amdgcn_sched_barrier(0);
     }
-    pf_prio<0>(w);
     if (!(RD4_PF_KNOB & 8) && RD4_PF_DMAPOS != 0) {
       if (RD4_PF_DMAPOS == 3 && blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
       if (blk + 2 < n_blocks) issue_k(blk + 2, ks2);
@@ -553,7 +542,6 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
     // ---- O^T += V^T P^T: A = 16 dims x 32 keys of V (k-slot 8g + j is key
     // 32kg + 16(j/4) + 4g + j%4, as in pf), two transposing loads per operand;
     // the next two dim tiles' operands are read while the current ones run.
-    pf_prio<2>(w);
     if (!RD4_PF_VEARLY) {
 #pragma unroll
       for (int t = 0; t < kPVD - 1; ++t) read_vb(t, t);
@@ -572,7 +560,6 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       }
       if (RD4_PF_SB & 2) __builtin_amdgcn_sched_barrier(0);
     }
-    pf_prio<0>(w);
 #if RD4_PF_PROBE
     // sensitivity probes (diagnostic builds only): extra independent work per block
     if (RD4_PF_PROBE & 1)
