@@ -101,6 +101,10 @@ constexpr int kQG = RD4_PF_QKG, kQD0 = RD4_PF_QKD;
 #endif
 // where K(j + 2) is requested (0 at the top of block j, 1 after its QK^T phase,
 // 3 with V(j + 1) after it too)
+// K/V DMA by inline asm (1) or by the builtin (0)
+#ifndef RD4_PF_DMAASM
+#define RD4_PF_DMAASM 1
+#endif
 #ifndef RD4_PF_DMAPOS
 #define RD4_PF_DMAPOS 1
 #endif
@@ -158,6 +162,21 @@ __device__ __forceinline__ float max_groups4_raw(float x) {
   float r;
   __asm__("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(c), "v"(d));
   return r;
+}
+
+// K/V block DMA through asm: the builtin makes the compiler put a vmcnt(0) in
+// front of later LDS reads it cannot tell from the DMA's destination (the
+// transposing V reads), i.e. wait for the next blocks' DMA; the kernel waits
+// for its DMA explicitly (s_waitcnt vmcnt at the top of each block). 16 bytes
+// per lane from saddr + voffset into LDS at M0 + 16 * lane.
+__device__ __forceinline__ void dma16(const uint8_t *sbase, uint32_t voff, uint32_t lds) {
+  __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                   :
+                   : "v"(voff), "s"(sbase), "s"(lds)
+                   : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p);
 }
 
 }  // namespace
@@ -333,7 +352,8 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
         if (!kEven && w * ND + r >= 32) break;
         uint32_t off = k_goff[r];
         __asm__("" : "+v"(off));  // keeps the offset 32-bit (no hoisted 64-bit copy)
-        __builtin_amdgcn_global_load_lds((const void *)(src + off), (lds_void *)(dst + (w * ND + r) * 1024), 16, 0, 0);
+        if (RD4_PF_DMAASM) dma16(src, off, lds_addr(dst + (w * ND + r) * 1024));
+        else __builtin_amdgcn_global_load_lds((const void *)(src + off), (lds_void *)(dst + (w * ND + r) * 1024), 16, 0, 0);
       }
     } else {  // last block: keys past kend re-read a valid row (masked later)
 #pragma unroll
@@ -342,9 +362,9 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
         const int c = (w * ND + r) * 64 + lane;
         const int key = c >> 5, slot = c & 31;
         const int jk = min(key, kend - j0);
-        __builtin_amdgcn_global_load_lds(
-            (const void *)(src + (uint32_t)(jk * (int)kvstride + 16 * (slot ^ swz(key)))),
-            (lds_void *)(dst + (w * ND + r) * 1024), 16, 0, 0);
+        const uint32_t off = (uint32_t)(jk * (int)kvstride + 16 * (slot ^ swz(key)));
+        if (RD4_PF_DMAASM) dma16(src, off, lds_addr(dst + (w * ND + r) * 1024));
+        else __builtin_amdgcn_global_load_lds((const void *)(src + off), (lds_void *)(dst + (w * ND + r) * 1024), 16, 0, 0);
       }
     }
   };
