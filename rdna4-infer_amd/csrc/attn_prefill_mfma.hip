@@ -181,6 +181,29 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
 
 }  // namespace
 
+#ifndef RD4_PF_TRACE
+#define RD4_PF_TRACE 0
+#endif
+#if RD4_PF_TRACE
+// timestamps (100 MHz realtime counter) of lane 0 of each wave of the first 64
+// CTAs (diagnostic builds only): [cta][wave][point]; point 0 the start, then 5
+// per block for the first 12 blocks (barrier passed, S^T MFMAs issued, softmax
+// start, PV start, PV issued)
+__device__ unsigned long long rd4_pf_trace[64 * 16 * 64];
+extern "C" int rd4_pf_trace_read(void *host) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(rd4_pf_trace), sizeof(rd4_pf_trace));
+}
+#define RD4_PFTP(pt)                                                                          \
+  do {                                                                                        \
+    if (lane == 0 && blockIdx.x < 64 && (pt) < 64)                                            \
+      rd4_pf_trace[(blockIdx.x * 16 + w) * 64 + (pt)] = __builtin_amdgcn_s_memrealtime();     \
+  } while (0)
+#else
+#define RD4_PFTP(pt) \
+  do {               \
+  } while (0)
+#endif
+
 // W waves of NSL 16-row slabs each (W * 16 * NSL rows per CTA).
 template <int W, int NSL>
 __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) {
@@ -200,6 +223,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
   const int grp = p.n_head / p.n_head_kv;
+  RD4_PFTP(0);
   const int n_rows = p.n_q * grp;
   const int n_rb = (n_rows + kBM - 1) / kBM;
   // XCD-aware order: workgroup L runs on XCD L % 8. When the kv heads divide
@@ -389,9 +413,8 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
 #pragma unroll
   for (int b = 0; b < 8; ++b) k_loff[b] = n * (kHD * 2) + 16 * ((4 * b + g) ^ swz(n));
 
-  // Issue order: K0 V0 K1, then in block j: V(j+1), K(j+2). At the top of block
-  // j the loads issued after V(j) are K(j+1)'s only, so waiting until at most
-  // those remain lands K(j) and V(j) and leaves K(j+1) in flight.
+  // Issue order: K0 V0 K1, then in block j: V(j+1) at the top, K(j+2) after
+  // the QK^T phase.
   if (n_blocks > 0) {
     issue_k(0, 0);
     issue_v(0, 0);
@@ -405,24 +428,17 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
 #endif
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int vs = blk & 1;
-    if (blk + 1 < n_blocks) {
-      // K(j), V(j) landed; K(j+1) (this wave's nk DMA instructions) may fly
-      if (kEven) {
-        __builtin_amdgcn_s_waitcnt((ND & 15) | ((ND >> 4) << 14) | (7 << 4) | (15 << 8));
-      } else {
-        const int nk = min(max(32 - w * ND, 0), ND);
-        if (nk >= 3) __builtin_amdgcn_s_waitcnt(3 | (7 << 4) | (15 << 8));
-        else if (nk == 2) __builtin_amdgcn_s_waitcnt(2 | (7 << 4) | (15 << 8));
-        else if (nk == 1) __builtin_amdgcn_s_waitcnt(1 | (7 << 4) | (15 << 8));
-        else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
-      }
-    } else {
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    // every wave's DMA for blk landed; every wave is done with blk - 1. A CTA
-    // barrier for LDS only: __syncthreads would also wait for K(blk + 1).
+    // every DMA this wave issued has landed: K(j), V(j) and also K(j+1), which
+    // was requested a block earlier and has landed by now (waiting for it costs
+    // nothing measurable). A partial count would assume that the DMA completes
+    // in order with any other vector-memory load the compiler places in the loop
+    // (spill reloads), which it does not know about.
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // every wave's DMA for blk landed; every wave is done with blk - 1 (a CTA
+    // barrier on LDS only, in asm)
 #ifndef RD4_PF_FULLBAR
     if (!(RD4_PF_KNOB & 16)) __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (blk < 12) RD4_PFTP(5 * blk + 1);
 #else
     __syncthreads();
 #endif
@@ -470,6 +486,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
                     : __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][f & 7], s[sl][kt], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (blk < 12) RD4_PFTP(5 * blk + 2);
     half8 vb[kPVD][2];
     // step t: key group kg = t / 8, dim tiles 2(t % 8), +1
     auto read_vb = [&](int buf, int t) {
@@ -496,6 +513,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       if (blk + 2 < n_blocks) issue_k(blk + 2, ks2);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (blk < 12) RD4_PFTP(5 * blk + 3);
     // ---- online softmax per slab: lane = row n, keys 16kt + 4g + i
     half8 pf[NSL][2];
     if (RD4_PF_KNOB & 4) {
@@ -559,6 +577,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
 #pragma unroll
         for (int i = 0; i < 8; ++i) pf[sl][kg][i] = (_Float16)s[sl][2 * kg + (i >> 2)][i & 3];
     }
+    if (blk < 12) RD4_PFTP(5 * blk + 4);
     // ---- O^T += V^T P^T: A = 16 dims x 32 keys of V (k-slot 8g + j is key
     // 32kg + 16(j/4) + 4g + j%4, as in pf), two transposing loads per operand;
     // the next two dim tiles' operands are read while the current ones run.
@@ -580,6 +599,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       }
       if (RD4_PF_SB & 2) __builtin_amdgcn_sched_barrier(0);
     }
+    if (blk < 12) RD4_PFTP(5 * blk + 5);
 #if RD4_PF_PROBE
     // sensitivity probes (diagnostic builds only): extra independent work per block
     if (RD4_PF_PROBE & 1)
