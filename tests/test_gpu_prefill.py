@@ -50,6 +50,8 @@ def test_fa2_entry_point(rd4, orc, dev):
     (16, 2, 50, 129, False, False),  # group 8, f32 queries, no gate
     (4, 4, 7, 65, True, True),       # group 1 (MHA)
     (24, 4, 1000, 512, True, False), # the reference's chunk size
+    (6, 3, 40, 300, True, True),     # 3 kv heads (the CTA order without the XCD map)
+    (16, 8, 5, 97, False, True),     # 8 kv heads, group 2
 ])
 def test_prefill_shapes(rd4, orc, dev, nh, nkv, pos0, nq, q_f16, gated):
     import torch
