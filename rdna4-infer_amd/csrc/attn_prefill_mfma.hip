@@ -93,7 +93,7 @@ constexpr int kQG = RD4_PF_QKG, kQD0 = RD4_PF_QKD;
 #endif
 // the first PV operand reads go out before the softmax (1) or after it (0)
 #ifndef RD4_PF_VEARLY
-#define RD4_PF_VEARLY 1
+#define RD4_PF_VEARLY 0
 #endif
 // causal mask under a wave-uniform branch (1) or applied to every block (0)
 #ifndef RD4_PF_MASKBR
