@@ -19,6 +19,14 @@
 
 namespace rd4 {
 
+// f32 multiply / add / subtract, each rounded on its own. They are written
+// here, under this file's `fp contract(off)`, so no caller can have them fused
+// into an FMA: HIP's __fmul_rn / __fadd_rn are defined before that pragma with
+// contraction allowed, and a product of one feeding the other does get fused.
+__device__ __forceinline__ float mul_rn(float a, float b) { return a * b; }
+__device__ __forceinline__ float add_rn(float a, float b) { return a + b; }
+__device__ __forceinline__ float sub_rn(float a, float b) { return a - b; }
+
 enum KvType : int { F32 = 0, F16 = 1, Q8_0 = 2, Q4_0 = 3, Q5_0 = 4, Q4_1 = 5 };
 constexpr int kNumTypes = 6;
 

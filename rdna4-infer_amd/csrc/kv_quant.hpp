@@ -4,8 +4,9 @@
 // llama.cpp's quantize_row_{q8_0,q4_0,q5_0,q4_1}_ref. One 32-element block per
 // 8-lane group, 4 elements per lane; statistics are reduced with xor shuffles
 // (order independent, or carrying the element index for the first-occurrence
-// tie-break), and every f32 step is an explicit round-to-nearest intrinsic so
-// nothing is contracted into an FMA. The bytes equal the serial loop's.
+// tie-break), and every f32 step is rounded on its own (mul_rn / add_rn /
+// sub_rn, never fused into an FMA), as in the reference's host mirror and
+// llama.cpp's reference quantizers. The bytes equal the serial loop's.
 #pragma once
 #include "common.hpp"
 
@@ -55,7 +56,7 @@ __device__ __forceinline__ void quant_block8(const float x[4], int sub, uint8_t 
     const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
     uint32_t w = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w |= ((uint32_t)(uint8_t)(int8_t)(int)roundf(__fmul_rn(x[i], id))) << (8 * i);
+    for (int i = 0; i < 4; ++i) w |= ((uint32_t)(uint8_t)(int8_t)(int)roundf(mul_rn(x[i], id))) << (8 * i);
     if (sub == 0) st_u16(blk, f2h(d));
     st_u16(blk + 2 + 4 * sub, (uint16_t)w);
     st_u16(blk + 4 + 4 * sub, (uint16_t)(w >> 16));
@@ -69,7 +70,7 @@ __device__ __forceinline__ void quant_block8(const float x[4], int sub, uint8_t 
     uint32_t nib = 0, bits = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int q = trunc_i8_clamp(__fadd_rn(__fmul_rn(x[i], id), kOff), kMax);
+      const int q = trunc_i8_clamp(add_rn(mul_rn(x[i], id), kOff), kMax);
       nib |= (uint32_t)(q & 15) << (8 * i);
       bits |= (uint32_t)(q >> 4) << (4 * sub + i);
     }
@@ -98,12 +99,12 @@ __device__ __forceinline__ void quant_block8(const float x[4], int sub, uint8_t 
       lo = fminf(lo, xor_f(lo, m));
       hi = fmaxf(hi, xor_f(hi, m));
     }
-    const float d = __fdiv_rn(__fsub_rn(hi, lo), 15.0f);
+    const float d = __fdiv_rn(sub_rn(hi, lo), 15.0f);
     const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
     uint32_t nib = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int q = trunc_i8_clamp(__fadd_rn(__fmul_rn(__fsub_rn(x[i], lo), id), 0.5f), 15);
+      const int q = trunc_i8_clamp(add_rn(mul_rn(sub_rn(x[i], lo), id), 0.5f), 15);
       nib |= (uint32_t)q << (8 * i);
     }
     const uint32_t hi_nib = xor_u(nib, 4);

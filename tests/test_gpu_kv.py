@@ -82,3 +82,19 @@ def test_store_width_is_block_local(rd4, orc, dev):
     dst = torch.empty(n // 32 * 34, dtype=torch.uint8, device=dev)
     rd4.kv_store_rows(2, to_dev(x, torch, dev), dst)
     assert np.array_equal(dst.cpu().numpy(), orc.store_rows(2, x))
+
+
+def test_store_rounding_order_pins(rd4, orc, dev):
+    """The GPU quantizer on the rounding-order blocks of tests/quant_pins.py
+    (x*(1/d) and a separate offset add, as the reference): the same codes as
+    the exact derivation."""
+    import torch
+    import quant_pins as qp
+    for kind, vals, t in (("q8_0", qp.Q8_0_BLOCK, orc.Q8_0), ("q4_0", qp.Q4_0_BLOCK, orc.Q4_0),
+                          ("q5_0", qp.Q5_0_BLOCK, orc.Q5_0), ("q4_1", qp.Q4_1_BLOCK, orc.Q4_1)):
+        x = qp.block(vals)
+        want = qp.q8_0_codes(x)[0] if kind == "q8_0" else qp.nib_codes(kind, x)[0]
+        nb = orc.row_bytes(t, 32)
+        dst = torch.full((nb,), 0xAB, dtype=torch.uint8, device=dev)
+        rd4.kv_store_rows(t, to_dev(x, torch, dev), dst)
+        assert qp.decode_codes(kind, dst.cpu().numpy()) == want, kind

@@ -424,3 +424,28 @@ def test_rms_norm_matches_f64(orc):
         x64 = x.astype(np.float64)
         want = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + eps) * w
         assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
+
+
+# ------------------------------------------ rounding-order pins (x*(1/d), separate add) --
+
+def test_quantizer_rounding_order_pins(orc):
+    """Blocks where the reference's order (id = 1/d, x*id rounded, then the
+    offset added and rounded) gives other codes than x/d or a fused add: the
+    oracle must produce the codes of the reference order, derived by exact
+    rational arithmetic in tests/quant_pins.py."""
+    import quant_pins as qp
+    x8 = qp.block(qp.Q8_0_BLOCK)
+    ref, div = qp.q8_0_codes(x8)
+    assert ref[1:5] == [-19, -61, 64, 96]            # worked out exactly, see quant_pins
+    assert ref != div                                 # x/d would change codes here
+    assert qp.decode_codes("q8_0", orc.store_rows(orc.Q8_0, x8)) == ref
+    for kind, vals, t in (("q4_0", qp.Q4_0_BLOCK, orc.Q4_0), ("q5_0", qp.Q5_0_BLOCK, orc.Q5_0),
+                          ("q4_1", qp.Q4_1_BLOCK, orc.Q4_1)):
+        x = qp.block(vals)
+        ref, fused, div = qp.nib_codes(kind, x)
+        assert ref != fused and ref != div, kind      # both alternatives are caught
+        assert qp.decode_codes(kind, orc.store_rows(t, x)) == ref, kind
+    # the literal codes of the discriminating elements
+    assert qp.nib_codes("q4_0", qp.block(qp.Q4_0_BLOCK))[0][1:4] == [12, 8, 11]
+    assert qp.nib_codes("q5_0", qp.block(qp.Q5_0_BLOCK))[0][1:5] == [14, 23, 30, 18]
+    assert qp.nib_codes("q4_1", qp.block(qp.Q4_1_BLOCK))[0][2:6] == [1, 11, 7, 8]
