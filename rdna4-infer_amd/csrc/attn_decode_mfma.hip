@@ -816,16 +816,24 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   } while (0)
 #endif
   RD4_TP();
+  if (RD4_DEC_KNOBS && (a.dbg & 4096)) return;  // profiling: launch cost alone
   const int grp = a.n_head / a.n_head_kv;
   const int h0 = kvh * grp + hc * kG;
   const int G = min(kG, grp - hc * kG);
   const int t = a.pos ? a.pos[tok] : a.t + tok + ntc - 1;  // last key of the CTA's last token
   const int n_keys = t + 1;
 
+#ifndef RD4_DEC_ILV
+#define RD4_DEC_ILV 1
+#endif
+  // Keys of split s: with RD4_DEC_ILV, the 16-key tiles s, s + S, s + 2S, ...
+  // (at any moment the splits of a kv head read neighbouring tiles); else a
+  // contiguous range of tiles.
   int chunk = (max(n_keys, 0) + a.n_splits - 1) / a.n_splits;
   chunk = (chunk + kTile - 1) / kTile * kTile;
-  const int j_begin = s * chunk;
-  const int j_end = min(n_keys, j_begin + chunk);
+  const int j_begin = RD4_DEC_ILV ? 16 * s : s * chunk;
+  const int j_end = RD4_DEC_ILV ? max(n_keys, 0) : min(n_keys, j_begin + chunk);
+  const int j_step = RD4_DEC_ILV ? 16 * a.n_splits : 16;  // keys between the split's tiles
 
   const int64_t kstride = (int64_t)a.n_head_kv * rowb<KT>();
   const int64_t vstride = (int64_t)a.n_head_kv * rowb<VT>();
@@ -835,7 +843,8 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   // Fused append: the CTA owning key t writes the new K/V row of its kv head
   // (8-lane groups per 32-element block, the store kernel's quantizer) before
   // any of its tiles is requested; every other CTA starts its loads at once.
-  const bool owns_new = a.k_new && j_begin <= t && t < j_end;
+  const bool owns_new = a.k_new && t >= 0 &&
+                        (RD4_DEC_ILV ? (t >> 4) % a.n_splits == s : (j_begin <= t && t < j_end));
   if (owns_new) {
     if (tid < 128) {
       const bool isv = tid >= 64;
@@ -871,7 +880,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   float *dv_t = dk_t + 128 * (iDV > 0 ? iDV : 0);
   float *mk_t = dk_t + 128 * (iMK > 0 ? iMK : 0);
   float *mv_t = dk_t + 128 * (iMV > 0 ? iMV : 0);
-  const int n_tiles_all = (j_end - j_begin + kTile - 1) / kTile;
+  const int n_tiles_all = j_end > j_begin ? (j_end - j_begin - 1) / j_step + 1 : 0;
   // Tile order: with 8 waves, waves w and w + 4 share a SIMD and the older one
   // (w < 4) is issued first, so it takes more tiles: n_lo rounds go to all 8
   // waves (tile 8i + w), the rest to waves 0-3 only (4 per round).
@@ -918,7 +927,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   }
   auto issue = [&](int i) {  // i-th tile of this wave
     if (RD4_DEC_KNOBS && (a.dbg & 2048)) return;
-    const int j0 = j_begin + tile_of(i) * kTile;
+    const int j0 = j_begin + tile_of(i) * j_step;
     const int nk = min(kTile, j_end - j0);
     const uint8_t *kt0 = kbase + (int64_t)j0 * kstride;
     const uint8_t *vt0 = vbase + (int64_t)j0 * vstride;
@@ -1013,6 +1022,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     if constexpr (!kI8) __syncthreads();
   }
   RD4_TP();
+  if (RD4_DEC_KNOBS && (a.dbg & 8192)) return;  // profiling: up to the query rows
   // One tile requested as soon as the query rows are in (on the LDS-staged query
   // paths, once every wave has read them), so it lands during the query
   // preparation. The preparation's barriers wait for LDS only: a CTA barrier
@@ -1338,12 +1348,13 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   // compiler gives every MFMA a result register apart from its C operand and
   // copies all 64 back on every tile.)
   RD4_TP();
+  if (RD4_DEC_KNOBS && (a.dbg & 16384)) return;  // profiling: up to the tile loop
   int i = 0;
   for (;;) {
     bool rescale_due = false;
     for (; i < my_tiles; ++i) {
       RD4_TP();
-      const int j_tile = j_begin + tile_of(i) * kTile;
+      const int j_tile = j_begin + tile_of(i) * j_step;
       const int nk = min(kTile, j_end - j_tile);
       if (next_issue <= i + R - 1 && next_issue < my_tiles) {
         // the stage being refilled was read by the previous iteration: those reads are done
@@ -1533,6 +1544,10 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   }
 
   RD4_TP();
+  if (RD4_DEC_KNOBS && (a.dbg & 32768)) {  // profiling: no epilogue (a store keeps the loop live)
+    if (m_run == 1.2345f) a.out[lane] = l_run + o[0][0] + o[15][3];
+    return;
+  }
   // ---- wave state: l summed over the 4 key groups; the hi (n < 8) and lo
   // (n >= 8) rows of O go to LDS as separate rows and are added by the reader
   l_run = sum_groups4(l_run);
@@ -1586,7 +1601,6 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   }
   __syncthreads();
   RD4_TP();
-  float *ms = wo + kWaves * 16 * kRowPad;  // in-kernel merge tree's LDS (flag and tables) past this
 
   // output rows: (token tr, head hh) in MFMA row r = hh + 8 tr. Each thread
   // weighs the 8 wave states of its row itself (one LDS round trip for their m
@@ -1625,10 +1639,6 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         }
         a.out[oi] = o1;
       }
-    } else if (!pair && a.mrec) {
-      // in-kernel slice merge: the record goes to the slice that holds (hh, d)
-      slice_record_store(a, ((tok * a.n_head_kv + kvh) * a.n_chunks + hc), s, hh * kHD + d, kHD,
-                         make_float4(acc4[0], acc4[1], acc4[2], acc4[3]), mm, L);
     } else {
       *(floatx4 *)(rec_acc(a, hrow_r, s) + d) = acc4;
       if (d == 0) {
@@ -1639,20 +1649,6 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     }
   }
   RD4_TP();
-  if (a.n_splits == 1) return;
-  if (!pair && a.mrec) {
-#if RD4_DEC_TRACE
-    slice_merge<kThreads>(a, (tok * a.n_head_kv + kvh) * a.n_chunks + hc, tok, h0, G, s, ms,
-                          tcta < 1024 ? &rd4_dec_trace[(tcta * 8 + w) * 32] : nullptr);
-#else
-    slice_merge<kThreads>(a, (tok * a.n_head_kv + kvh) * a.n_chunks + hc, tok, h0, G, s, ms);
-#endif
-    return;
-  }
-  int *flag = (int *)(ms + 2 * kR + kWaves * kR);
-  if (pair || a.ext_merge || (a.dbg & 1)) return;
-  split_tail<kThreads>(a, tok, kvh, hc, h0, G, s, flag, (float *)(flag + 4),
-                       (float *)(flag + 4) + kGMaxMerge * kMergeFan);
 }
 
 namespace {
@@ -1663,10 +1659,8 @@ size_t decode_lds() {
   // query rows (later the shared fragments and the q4_1 block sums)
   const size_t qreg = (size_t)kG * (kHD * 4 + 16) + 256 + TS::QI;
   const size_t tiles = (size_t)TS::WAVES * TS::R * TS::TB + qreg;  // scale tables are static LDS
-  // (past the wave states: the in-kernel tree's flag and tables, or the slice
-  // merge's 64 (m, l) quads)
-  const size_t tail = (2 * 16 + TS::WAVES * 16 + 4 + kGMaxMerge * kMergeFan + 2 * kGMaxMerge) * 4;
-  const size_t merge = (2 * TS::WAVES * 16 + TS::WAVES * 16 * kRowPad) * 4 + (tail > 1040 ? tail : 1040);
+  // the wave states of the epilogue reuse the ring
+  const size_t merge = (2 * TS::WAVES * 16 + TS::WAVES * 16 * kRowPad) * 4;
   return tiles > merge ? tiles : merge;
 }
 
@@ -1690,6 +1684,7 @@ bool hot_v(int t) { return t == F16 || t == Q8_0 || t == Q4_0 || t == Q5_0 || t 
 }  // namespace
 
 bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim) {
+  // read per call: the tests switch paths inside one process
   const char *e = std::getenv("RD4_DECODE_GENERIC");
   if (e && std::atoi(e) != 0) return false;
   return hot_k(kt) && hot_v(vt) && head_dim == kHD && n_head_kv > 0 &&
@@ -1697,18 +1692,6 @@ bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_d
 }
 
 bool decode_mfma_pairs(int kt, int vt) { return pair_type(kt, vt); }
-
-bool decode_mfma_ext_merge() {
-  // Split records are merged by a second, short launch: a kernel boundary makes
-  // them visible for about one launch gap, where an in-kernel tree pays a
-  // device-scope atomic plus a record round trip per level (RD4_DECODE_MERGE=2
-  // selects the tree, for measurements).
-  static const bool tree = [] {
-    const char *e = std::getenv("RD4_DECODE_MERGE");
-    return e && std::atoi(e) == 2;
-  }();
-  return !tree;
-}
 
 hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hipStream_t st) {
   AttnArgs a = a0;
@@ -1719,9 +1702,8 @@ hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a0, int n_tok, hip
   if (a.tok_pair && (a.pos || a.k_new || a.q_f16 || a.n_chunks != 1 || n_tok < 2 ||
                      !pair_type(kt, vt)))
     a.tok_pair = 0;
-  // (a caller may ask for the merge launch by setting ext_merge beforehand)
-  if (a.tok_pair) a.mrec = nullptr;  // pair CTAs hand their records to the merge launch
-  a.ext_merge = (a.n_splits > 1 && !a.mrec && (a.tok_pair || a.ext_merge || decode_mfma_ext_merge())) ? 1 : 0;
+  // split records are folded by the merge launch on the same stream
+  a.ext_merge = a.n_splits > 1 ? 1 : 0;
   const int grid_tok = a.tok_pair ? (n_tok + 1) / 2 : n_tok;
   hipError_t err = hipErrorInvalidValue;
 #define RD4_D(K, V) \

@@ -6,12 +6,6 @@ namespace rd4 {
 
 // Split count ceiling of the library's partial scratch per (token, head).
 constexpr int kMaxSplits = 256;
-// A signalling-NaN bit pattern no arithmetic result can take (results are
-// quiet NaNs): marks a record slot of the in-kernel merge as not yet written.
-constexpr uint32_t kPoison = 0x7FBADBADu;
-// In-kernel merge limits: splits (one per lane of a wave) and slice values.
-constexpr int kInMergeMaxSplits = 64;
-constexpr int kInMergeMaxZ = 64;
 
 struct AttnArgs {
   const float *q;         // [n_tok][n_head][hd] f32 (or f16 when q_f16)
@@ -37,12 +31,6 @@ struct AttnArgs {
   int n_chunks;
   int k_lds_stride, v_lds_stride;
   int ext_merge;  // 1: the kernel only writes level-0 records; merge_splits_launch merges
-  // In-kernel slice merge (MFMA decode, single-token CTAs): split records go to
-  // mrec, a region of uncached scratch that holds kPoison wherever no record is
-  // pending; CTA s then merges output slice s (merge_z values of its head chunk)
-  // and restores kPoison over what it read. mrec == nullptr: not used.
-  float *mrec;
-  int merge_z, merge_slices;
   // MFMA decode only: 1 = each CTA carries two consecutive tokens (query rows
   // 0-7 the first token's heads, 8-15 the second's, f16 queries), positions
   // t + token; n_tok is the token count of the launch

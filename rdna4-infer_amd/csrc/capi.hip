@@ -60,19 +60,17 @@ bool valid_type(int t) { return t >= 0 && t < kNumTypes; }
 // records fit (see run_attn).
 constexpr int64_t kPartialFloats = 16ll << 20;  // 64 MiB of records per stream
 constexpr int64_t kCounterWords = 1 << 20;
-constexpr int64_t kMergeRecFloats = 4ll << 20;  // 16 MiB: the in-kernel slice merge's records
 struct Scratch {
   float *partial = nullptr;    // uncached: records exchanged between CTAs inside a launch
   float *partial_c = nullptr;  // cached: records handed to a later launch
   unsigned *counters = nullptr;
-  float *mrec = nullptr;       // uncached, kPoison wherever no record is pending
 };
 std::map<std::pair<int, uintptr_t>, Scratch> g_scratch;
 std::map<int, std::vector<Scratch>> g_spare;  // per device, made by rd4_init, not yet assigned
 std::mutex g_scratch_mu;
 
-// A new set on the current device; its counters are zeroed and its merge
-// records set to kPoison by fill kernels on `st` (waited for when `blocking`).
+// A new set on the current device; its counters are zeroed by a fill kernel on
+// `st` (waited for when `blocking`).
 int new_scratch(hipStream_t st, bool blocking, Scratch *out) {
   Scratch n;
   // Uncached: the generic kernel's split records cross XCDs inside one launch
@@ -80,31 +78,13 @@ int new_scratch(hipStream_t st, bool blocking, Scratch *out) {
   if (hipExtMallocWithFlags((void **)&n.partial, kPartialFloats * sizeof(float),
                             hipDeviceMallocUncached) != hipSuccess ||
       hipMalloc(&n.partial_c, kPartialFloats * sizeof(float)) != hipSuccess ||
-      hipMalloc(&n.counters, kCounterWords * sizeof(unsigned)) != hipSuccess ||
-      hipExtMallocWithFlags((void **)&n.mrec, kMergeRecFloats * sizeof(float), hipDeviceMallocUncached) !=
-          hipSuccess)
+      hipMalloc(&n.counters, kCounterWords * sizeof(unsigned)) != hipSuccess)
     return fail(RD4_ENOMEM, "scratch allocation failed%s");
   const bool ok = fill_u32_launch(n.counters, kCounterWords, 0u, st) == hipSuccess &&
-                  fill_u32_launch((uint32_t *)n.mrec, kMergeRecFloats, kPoison, st) == hipSuccess &&
                   (!blocking || hipStreamSynchronize(st) == hipSuccess);
   if (!ok) return fail(RD4_ELAUNCH, "scratch counter fill failed%s");
   *out = n;
   return RD4_OK;
-}
-
-// Compute units of the current device (cached per device).
-int device_cus() {
-  static std::mutex mu;
-  static std::map<int, int> cus;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  std::lock_guard<std::mutex> lk(mu);
-  auto it = cus.find(dev);
-  if (it != cus.end()) return it->second;
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
-  cus[dev] = n;
-  return n;
 }
 
 int current_device(int *dev) {
@@ -149,10 +129,11 @@ int check_attn_shape(int n_head, int n_head_kv, int head_dim, int kt, int vt) {
 // (the MFMA kernel's CTA fills a CU; the generic kernel's takes a quarter of
 // one), and at least `min_keys` keys per split.
 int auto_splits(int keys, int ctas_per_split, int target, int min_keys) {
-  if (const char *e = std::getenv("RD4_DECODE_SPLITS")) {  // tuning override
-    const int v = std::atoi(e);
-    if (v >= 1) return v > kMaxSplits ? kMaxSplits : v;
-  }
+  static const int env = [] {  // tuning override, read once
+    const char *e = std::getenv("RD4_DECODE_SPLITS");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (env >= 1) return env > kMaxSplits ? kMaxSplits : env;
   int s = (target + ctas_per_split - 1) / ctas_per_split;
   const int by_keys = (keys + min_keys - 1) / min_keys;
   if (s > by_keys) s = by_keys;
@@ -245,8 +226,10 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
       a.dbg = 0;
       return launched(decode_mfma_launch(kt, vt, a, n_tok, st), "decode kernel");
     }
-    const bool ext = mfma && decode_mfma_ext_merge();
-    const bool use_caller = ext && caller_partial && splits <= caller_splits;
+    const bool ext = mfma;  // the MFMA decode merges its records in a second launch
+    // (its records are stored as 16-byte vectors: a misaligned buffer is not used)
+    const bool use_caller = ext && caller_partial && splits <= caller_splits &&
+                            ((uintptr_t)caller_partial & 15) == 0;
     if (!use_caller) {
       // level-0 (+ level-1) records and the counters must fit the stream's scratch
       auto fits = [&](int S, int64_t ntok) {
@@ -289,29 +272,6 @@ int run_attn(const float *q, const void *k, const void *v, float *out, float *ga
       // suffices); the in-kernel merge tree needs the uncached one.
       a.partial = ext ? s->partial_c : s->partial;
       a.counters = s->counters;
-      // RD4_DECODE_MERGE=3: the in-kernel slice merge (one launch) for
-      // single-token MFMA CTAs when every CTA of the grid is resident at once
-      // (one CTA per CU), each slice fits a wave's lanes, and the records fit
-      // the region. Measured about 0.5 us per step slower than the merge launch
-      // (the default) at 32K q8_0, so it is kept for comparison only.
-      static const int merge_mode = [] {
-        const char *e = std::getenv("RD4_DECODE_MERGE");
-        return e ? std::atoi(e) : 0;
-      }();
-      if (mfma && merge_mode == 3 && !(tok_pair && n_tok >= 2) && splits <= kInMergeMaxSplits) {
-        const int G = n_head / n_head_kv < 8 ? n_head / n_head_kv : 8;
-        const int vals = G * head_dim;
-        const int Z = ((vals + splits - 1) / splits + 3) / 4 * 4;
-        const int nsl = (vals + Z - 1) / Z;
-        const int64_t groups = (int64_t)n_tok * n_head_kv * n_chunks;
-        const int64_t ctas = groups * splits;
-        const int cus = device_cus();
-        if (Z <= kInMergeMaxZ && cus > 0 && ctas <= cus && groups * nsl * splits * (4 + Z) <= kMergeRecFloats) {
-          a.mrec = s->mrec;
-          a.merge_z = Z;
-          a.merge_slices = nsl;
-        }
-      }
     }
     a.acc1_off = a.ml0_off + rows * splits * 2;
     a.acc1_off = (a.acc1_off + 3) / 4 * 4;  // 16-byte aligned level-1 records

@@ -3,21 +3,35 @@
 //
 // The split kernel's level-0 records (m_s in ln units, l_s, acc_s[hd]) are
 // visible to this launch without any fence (kernel boundary). One 64-lane CTA
-// per (token, head, 64-dim quarter): every lane folds the weights of all splits
-// (m, l pairs read once per lane group), then lane (c, sub) sums the float4
-// column c over splits sub, sub + 4, ...; the four partial sums meet through
-// lane exchanges. All record loads of a lane are issued before they are used,
-// so the merge costs about one memory round trip.
+// per (token, head, 16-dim group): lane (c, sub) = (lane & 3, lane >> 2) owns
+// float4 c of the group for splits sub, sub + 16, ..., and loads those records
+// and their (m, l) pairs in one batch, with the gate logits, before using any
+// of them. Every split's m is then in some lane, so the max, the weights and
+// the sum l come from lane exchanges (DPP and the row / half-wave swaps)
+// without LDS, and the 16 split classes of a float4 meet the same way. The
+// merge costs one memory round trip plus a short dependent chain; the grid
+// (n_head * hd / 16 CTAs per token, 384 at 24 heads) spreads the loads over
+// the CUs.
 #include "merge.hpp"
 
 namespace rd4 {
 
 namespace {
 
-constexpr int kQuarterDims = 64;
+constexpr int kGroupDims = 16;
+constexpr int kPerLane = kMaxSplits / 16;  // record slots per lane
 
+// x + the value of lane (l + 4) % 16 and (l + 8) % 16 of its 16-lane row:
+// the sum over the four lanes of the row with the same l % 4
+__device__ __forceinline__ float sum_row_stride4(float x) {
+  int v = __builtin_bit_cast(int, x);
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xF, 0xF, false));  // row_ror:4
+  v = __builtin_bit_cast(int, x);
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xF, 0xF, false));  // row_ror:8
+  return x;
+}
 // x summed over lanes l, l ^ 16, l ^ 32, l ^ 48
-__device__ __forceinline__ float sum_groups4(float x) {
+__device__ __forceinline__ float sum_rows(float x) {
   float a = x, b = x;
   swap16(a, b);
   float c = a + b, d = c;
@@ -25,72 +39,62 @@ __device__ __forceinline__ float sum_groups4(float x) {
   return c + d;
 }
 
+#ifndef RD4_MERGE_EXP
+#define RD4_MERGE_EXP 0
+#endif
 __global__ __launch_bounds__(64) void merge_splits_kernel(AttnArgs a) {
-  __shared__ float w_s[kMaxSplits];
+  if (RD4_MERGE_EXP == 1) return;  // timing experiment: launch cost alone
   const int lane = threadIdx.x;
   const int hd = a.head_dim, S = a.n_splits;
-  const int nq = hd / kQuarterDims;
-  const int head = blockIdx.x / nq, quarter = blockIdx.x - head * nq;
+  const int ng = hd / kGroupDims;
+  const int head = blockIdx.x / ng, grp = blockIdx.x - head * ng;
   const int tok = blockIdx.y;
   const int64_t hrow = (int64_t)tok * a.n_head + head;
+  const int c = lane & 3, sub = lane >> 2;
+  const float *acc = a.partial + hrow * S * hd + kGroupDims * grp + 4 * c;
   const float *ml = a.partial + a.ml0_off + hrow * S * 2;
+  const int64_t oi = hrow * hd + kGroupDims * grp + 4 * c;
 
-  // record loads first (the first kBatch splits of this lane), then (m, l)
-  const int c = lane & 15, sub = lane >> 4;
-  const float *acc = a.partial + hrow * S * hd + quarter * kQuarterDims + 4 * c;
-  constexpr int kBatch = 16;
-  float4 v[kBatch];
+  // every load first: records and (m, l) of splits sub + 16 b, the gate logits
+  float4 v[kPerLane];
+  float2 r[kPerLane];
 #pragma unroll
-  for (int b = 0; b < kBatch; ++b) {
-    const int s = sub + 4 * b;
-    v[b] = s < S ? *(const float4 *)(acc + (int64_t)s * hd) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int b = 0; b < kPerLane; ++b) {
+    const int s = sub + 16 * b;
+    v[b] = make_float4(0.f, 0.f, 0.f, 0.f);
+    r[b] = make_float2(-INFINITY, 0.0f);
+    if (16 * b < S && s < S) {  // (16 b < S is uniform: slots past the count issue nothing)
+      v[b] = *(const float4 *)(acc + (int64_t)s * hd);
+      r[b] = *(const float2 *)(ml + 2 * s);
+    }
   }
-  const int64_t oi = hrow * hd + quarter * kQuarterDims + 4 * c;
   const float4 gl = (a.gate && sub == 0) ? *(const float4 *)(a.gate + oi) : make_float4(0.f, 0.f, 0.f, 0.f);
-  float mv[kMaxSplits / 64], lv[kMaxSplits / 64];
-#pragma unroll
-  for (int i = 0; i < kMaxSplits / 64; ++i) {
-    const int s = lane + 64 * i;
-    const float2 r = s < S ? *(const float2 *)(ml + 2 * s) : make_float2(-INFINITY, 0.0f);
-    mv[i] = r.x;
-    lv[i] = r.y;
-  }
+
   float mm = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < kMaxSplits / 64; ++i) mm = fmaxf(mm, mv[i]);
+  for (int b = 0; b < kPerLane; ++b)
+    if (16 * b < S) mm = fmaxf(mm, r[b].x);
   mm = wave_max(mm);
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
   float L = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kMaxSplits / 64; ++i) {
-    const int s = lane + 64 * i;
-    const float w = (mv[i] == -INFINITY) ? 0.0f : expf(mv[i] - mm);
-    if (s < S) w_s[s] = w;
-    L += w * lv[i];
+  for (int b = 0; b < kPerLane; ++b) {
+    if (16 * b >= S) continue;
+    // an empty split (m = -inf) weighs 0; so does every split when all are empty
+    const float w = (r[b].x == -INFINITY) ? 0.0f : expf(r[b].x - mm);
+    L = fmaf(w, r[b].y, L);
+    sum.x = fmaf(v[b].x, w, sum.x);
+    sum.y = fmaf(v[b].y, w, sum.y);
+    sum.z = fmaf(v[b].z, w, sum.z);
+    sum.w = fmaf(v[b].w, w, sum.w);
   }
-  L = wave_sum(L);
-  __syncthreads();
-  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s0 = sub;; s0 += 4 * kBatch) {
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const int s = s0 + 4 * b;
-      const float w = s < S ? w_s[s] : 0.0f;
-      sum.x += v[b].x * w;
-      sum.y += v[b].y * w;
-      sum.z += v[b].z * w;
-      sum.w += v[b].w * w;
-    }
-    if (s0 + 4 * kBatch >= S) break;
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const int s = s0 + 4 * kBatch + 4 * b;
-      v[b] = s < S ? *(const float4 *)(acc + (int64_t)s * hd) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
-  sum.x = sum_groups4(sum.x);
-  sum.y = sum_groups4(sum.y);
-  sum.z = sum_groups4(sum.z);
-  sum.w = sum_groups4(sum.w);
+  // the 16 split classes: lanes c + 4 sub of each row, then the four rows
+  sum.x = sum_rows(sum_row_stride4(sum.x));
+  sum.y = sum_rows(sum_row_stride4(sum.y));
+  sum.z = sum_rows(sum_row_stride4(sum.z));
+  sum.w = sum_rows(sum_row_stride4(sum.w));
+  // the lanes with c = 0 hold each split's l once
+  L = wave_sum(c == 0 ? L : 0.0f);
   if (sub != 0) return;
   const float inv = (mm == -INFINITY) ? 0.0f : ((L > 0.0f) ? 1.0f / L : 0.0f);
   float ov[4] = {sum.x * inv, sum.y * inv, sum.z * inv, sum.w * inv};
@@ -110,8 +114,9 @@ __global__ __launch_bounds__(64) void merge_splits_kernel(AttnArgs a) {
 }  // namespace
 
 hipError_t merge_splits_launch(const AttnArgs &a, int n_tok, hipStream_t st) {
-  if (a.head_dim % kQuarterDims != 0 || a.n_splits > kMaxSplits) return hipErrorInvalidValue;
-  dim3 grid((unsigned)(a.n_head * (a.head_dim / kQuarterDims)), (unsigned)n_tok);
+  if (a.head_dim % kGroupDims != 0 || a.n_splits > kMaxSplits) return hipErrorInvalidValue;
+  dim3 grid((unsigned)(a.n_head * (a.head_dim / kGroupDims)), (unsigned)n_tok);
+  if (RD4_MERGE_EXP == 2) return hipSuccess;  // timing experiment: no merge launch
   hipLaunchKernelGGL(merge_splits_kernel, grid, dim3(64), 0, st, a);
   return hipGetLastError();
 }

@@ -4,6 +4,9 @@
 // rope: attn.cuh:30-63 -- pair (p, p + n_rot/2) of each head rotates by
 // pos[t] * freq_base^(-2p/n_rot). Both are element-local, so a thread takes 4
 // consecutive elements (gate) or one pair (rope).
+#include <cstdio>
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace rd4 {
@@ -66,17 +69,21 @@ hipError_t fill_u32_launch(uint32_t *p, int64_t n, uint32_t v, hipStream_t st) {
 }
 
 // Streaming read of n16 16-byte words (bench calibration: the practical HBM
-// read rate of one launch). Grid-stride, four independent 16-byte loads in
-// flight per thread; the xor of everything is written only if it hits an
-// unlikely value, so the loads cannot be removed.
-__global__ __launch_bounds__(512) void read_probe_kernel(const uint4 *__restrict__ p, int64_t n16,
-                                                         uint32_t *__restrict__ sink) {
+// read rate of one launch). Grid-stride, U independent 16-byte loads in flight
+// per thread; the xor of everything is written only if it hits an unlikely
+// value, so the loads cannot be removed.
+template <int U>
+__global__ __launch_bounds__(1024) void read_probe_kernel(const uint4 *__restrict__ p, int64_t n16,
+                                                          uint32_t *__restrict__ sink) {
   uint32_t acc = 0;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i + 3 * stride < n16; i += 4 * stride) {
-    const uint4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
-    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  for (; i + (U - 1) * stride < n16; i += U * stride) {
+    uint4 x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = p[i + u * stride];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= x[u].x ^ x[u].y ^ x[u].z ^ x[u].w;
   }
   for (; i < n16; i += stride) {
     const uint4 a = p[i];
@@ -87,7 +94,20 @@ __global__ __launch_bounds__(512) void read_probe_kernel(const uint4 *__restrict
 
 hipError_t read_probe_launch(const void *p, int64_t bytes, uint32_t *sink, hipStream_t st) {
   if (bytes <= 0) return hipSuccess;
-  hipLaunchKernelGGL(read_probe_kernel, dim3(256), dim3(512), 0, st, (const uint4 *)p, bytes / 16, sink);
+  // shape "blocks,threads,loads" (RD4_PROBE, read once; measurement only)
+  static int shape[3] = {0, 0, 0};
+  static bool init = false;
+  if (!init) {
+    init = true;
+    if (const char *e = std::getenv("RD4_PROBE")) std::sscanf(e, "%d,%d,%d", &shape[0], &shape[1], &shape[2]);
+  }
+  // default: the fastest shape measured on MI355X for a 71 MB read (larger
+  // grids and more loads in flight per thread were slower)
+  const int nb = shape[0] > 0 ? shape[0] : 256, nt = shape[1] > 0 ? shape[1] : 512, u = shape[2] > 0 ? shape[2] : 4;
+  const uint4 *q = (const uint4 *)p;
+  if (u == 4) hipLaunchKernelGGL(read_probe_kernel<4>, dim3(nb), dim3(nt), 0, st, q, bytes / 16, sink);
+  else if (u == 16) hipLaunchKernelGGL(read_probe_kernel<16>, dim3(nb), dim3(nt), 0, st, q, bytes / 16, sink);
+  else hipLaunchKernelGGL(read_probe_kernel<8>, dim3(nb), dim3(nt), 0, st, q, bytes / 16, sink);
   return hipGetLastError();
 }
 

@@ -35,6 +35,5 @@ hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a, int n_tok, hipS
 // True when multi-token decode of this cache pair can put two tokens in a CTA.
 bool decode_mfma_pairs(int kt, int vt);
 // True when split records are merged by a second launch (not the in-kernel tree).
-bool decode_mfma_ext_merge();
 
 }  // namespace rd4

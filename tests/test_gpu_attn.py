@@ -18,7 +18,7 @@ def make_cache(orc, t, n, nkv, hd, seed, outlier=False):
 
 
 def run_decode(rd4, torch, dev, q, k, v, t, nh, nkv, hd, kt, vt, gate=None, n_splits=0):
-    out = torch.empty(nh * hd, dtype=torch.float32, device=dev)
+    out = torch.full((nh * hd,), float("nan"), dtype=torch.float32, device=dev)
     g = None if gate is None else to_dev(gate, torch, dev)
     rd4.attn_decode(to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev), out, t,
                     nh, nkv, hd, 1.0 / np.sqrt(hd), kt, vt, gate=g, n_splits=n_splits)
@@ -151,7 +151,7 @@ def test_batched(rd4, orc, dev, split):
     q = orc.randn(pos.size * nh * hd, 82).reshape(pos.size, nh, hd)
     want = orc.attn_batch(q, k, v, pos, nh, nkv, hd, 1 / 16, 2, 1)
     qd = to_dev(q, torch, dev)
-    out = torch.empty_like(qd)
+    out = torch.full_like(qd, float("nan"))  # unwritten elements stay NaN
     args = (qd, to_dev(k, torch, dev), to_dev(v, torch, dev), out, to_dev(pos, torch, dev), nh, nkv,
             hd, 1 / 16, 2, 1)
     if split:
@@ -205,7 +205,7 @@ def test_decode_append_fused(rd4, orc, dev, t, vt):
     q, g = orc.randn(nh * hd, 104), orc.randn(nh * hd, 105)
     gs, want = orc.sigmoid_gate(g, orc.attn_decode(q, k_ref, v_ref, n - 1, nh, nkv, hd, 1 / 16, t, vt).ravel())
     kd, vd, gd = to_dev(k, torch, dev), to_dev(v, torch, dev), to_dev(g, torch, dev)
-    out = torch.empty(nh * hd, device=dev)
+    out = torch.full((nh * hd,), float("nan"), device=dev)
     rd4.attn_decode_append(to_dev(q, torch, dev), to_dev(kn, torch, dev), to_dev(vn, torch, dev), kd, vd,
                            out, n - 1, nh, nkv, hd, 1 / 16, t, vt, gate=gd)
     torch.cuda.synchronize()
@@ -243,7 +243,7 @@ def test_baseline_decode_configs_full_size(rd4, orc, dev, cfg):
     v = make_cache(orc, vt, n, nkv, hd, 121, outlier=(kt == 2))
     q, g = orc.randn(nh * hd, 122), orc.randn(nh * hd, 123)
     kd, vd = to_dev(k, torch, dev), to_dev(v, torch, dev)
-    out = torch.empty(nh * hd, device=dev)
+    out = torch.full((nh * hd,), float("nan"), device=dev)
     gd = to_dev(g, torch, dev)
     if kt == 2:
         kn, vn = orc.randn(nkv * hd, 124), orc.randn(nkv * hd, 125)
@@ -281,7 +281,7 @@ v = to_dev(make_cache(orc, 2, n, nkv, hd, 501), torch, dev)
 q = to_dev(orc.randn(nh * hd, 502), torch, dev)
 outs = []
 for f in ("launch", "split", "forced"):
-    o = torch.empty(nh * hd, device=dev)
+    o = torch.full((nh * hd,), float("nan"), device=dev)
     if f == "launch":
         rd4.attn_launch(q, k, v, o, n - 1, nh, nkv, hd, 1 / 16, 2, 2)
     elif f == "split":
@@ -302,13 +302,12 @@ print("ok")
         assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
 
 
-@pytest.mark.parametrize("mode", ["2", "3"])
-def test_in_kernel_merge_env(mode):
-    """RD4_DECODE_MERGE=2 selects the in-kernel counter-tree merge of the split
-    records instead of the merge launch, 3 the in-kernel slice merge (both kept
-    for comparison). Each must match the oracle at 16 and 64 splits and repeat
-    bit for bit (the tree's counters reset themselves; the slice merge restores
-    its poison pattern). Child process: the library reads the variable once."""
+def test_in_kernel_merge_generic():
+    """RD4_DECODE_GENERIC=1 sends every pair to the all-types kernel, whose split
+    records are folded inside the launch by a counter tree (the MFMA decode uses
+    the merge launch). It must match the oracle at 16 and 64 splits and repeat
+    bit for bit (the tree's counters reset themselves). Child process: the
+    library reads the variable once."""
     import subprocess
     import sys
     import os
@@ -331,7 +330,7 @@ for kt, vt in ((2, 2), (3, 3), (1, 1)):
     for splits in (16, 64):
         outs = []
         for rep in range(2):
-            o = torch.empty(nh * hd, device=dev)
+            o = torch.full((nh * hd,), float("nan"), device=dev)
             rd4.attn_decode(q, k, v, o, n - 1, nh, nkv, hd, 1 / 16, kt, vt, n_splits=splits)
             torch.cuda.synchronize()
             outs.append(o.cpu().numpy())
@@ -340,7 +339,7 @@ for kt, vt in ((2, 2), (3, 3), (1, 1)):
 print("ok")
 '''
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    env = dict(os.environ, RD4_DECODE_MERGE=mode)
+    env = dict(os.environ, RD4_DECODE_GENERIC="1")
     r = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True, text=True,
                        timeout=180)
     assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
