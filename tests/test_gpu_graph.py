@@ -56,7 +56,7 @@ def test_decode_append_in_graph(rd4, orc, dev, kt):
     g0 = to_dev(orc.randn(NH * HD, 603), torch, dev)
     gate = g0.clone()
     kn, vn = to_dev(orc.randn(NKV * HD, 604), torch, dev), to_dev(orc.randn(NKV * HD, 605), torch, dev)
-    out = torch.empty(NH * HD, device=dev)
+    out = torch.full((NH * HD,), float("nan"), device=dev)
 
     def run():
         rd4.attn_decode_append(q, kn, vn, kc, vc, out, n - 1, NH, NKV, HD, 1 / 16, kt, vt, gate=gate)
@@ -73,7 +73,7 @@ def test_decode_tokens_in_graph(rd4, orc, dev):
     q = to_dev(orc.randn(n_tok * NH * HD, 612), torch, dev)
     g0 = to_dev(orc.randn(n_tok * NH * HD, 613), torch, dev)
     gate = g0.clone()
-    out = torch.empty(n_tok * NH * HD, device=dev)
+    out = torch.full((n_tok * NH * HD,), float("nan"), device=dev)
 
     def run():
         rd4.attn_decode_tokens(q, kc, vc, out, n - n_tok, n_tok, NH, NKV, HD, 1 / 16, 2, 2, gate=gate)
@@ -97,7 +97,7 @@ def test_epilogue_then_decode_in_graph(rd4, orc, dev):
     pos = to_dev(np.int32([t]), torch, dev)
     q = torch.empty(NH * HD, device=dev)
     gate = torch.empty_like(q)
-    out = torch.empty_like(q)
+    out = torch.full_like(q, float("nan"))  # unwritten elements stay NaN
 
     def run():
         rd4.qk_norm_rope_append(qg, kn, vn, qw, kw, 1e-6, 64, 1e7, pos, 1, NH, NKV, HD, q, kc, vc, 2, 2,

@@ -30,7 +30,7 @@ def _per_token(rd4, torch, dev, qd, kd, vd, t0, n_tok, kt, vt, splits):
     outs = []
     for i in range(n_tok):
         qi = qd[i * NH * HD:(i + 1) * NH * HD].clone()
-        oi = torch.empty_like(qi)
+        oi = torch.full_like(qi, float("nan"))  # unwritten elements stay NaN
         rd4.attn_decode(qi, kd, vd, oi, t0 + i, NH, NKV, HD, 1 / 16, kt, vt, n_splits=splits)
         outs.append(oi)
     torch.cuda.synchronize()
@@ -54,9 +54,9 @@ def test_tokens_vs_per_token_and_oracle(rd4, orc, dev, kt, vt, n_tok):
     splits = 6
     want = _per_token(rd4, torch, dev, qd, kd, vd, t0, n_tok, kt, vt, splits)
     pos = to_dev(np.arange(t0, n, dtype=np.int32), torch, dev)
-    out2 = torch.empty_like(qd)
+    out2 = torch.full_like(qd, float("nan"))  # unwritten elements stay NaN
     rd4.attn_split_batch(qd, kd, vd, out2, pos, NH, NKV, HD, 1 / 16, kt, vt, splits)
-    out = torch.empty_like(qd)
+    out = torch.full_like(qd, float("nan"))  # unwritten elements stay NaN
     rd4.attn_decode_tokens(qd, kd, vd, out, t0, n_tok, NH, NKV, HD, 1 / 16, kt, vt, n_splits=splits)
     torch.cuda.synchronize()
     assert np.array_equal(out2.cpu().numpy(), want)
@@ -78,7 +78,7 @@ def test_tokens_split_with_only_the_last_key(rd4, orc, dev, kt, vt):
     n, n_tok = 3009, 2
     k, v, kd, vd = _caches(orc, torch, dev, kt, vt, n, 320 + kt)
     q = orc.randn(n_tok * NH * HD, 330)
-    out = torch.empty(n_tok * NH * HD, device=dev)
+    out = torch.full((n_tok * NH * HD,), float("nan"), device=dev)
     rd4.attn_decode_tokens(to_dev(q, torch, dev), kd, vd, out, n - n_tok, n_tok, NH, NKV, HD, 1 / 16,
                            kt, vt, n_splits=189)
     torch.cuda.synchronize()
@@ -108,7 +108,7 @@ def test_draft_then_verify(rd4, orc, dev, kt, vt):
         if i < D:
             q = orc.randn(NH * HD, 350 + i)
             g = orc.randn(NH * HD, 360 + i)
-            out = torch.empty(NH * HD, device=dev)
+            out = torch.full((NH * HD,), float("nan"), device=dev)
             gd = to_dev(g, torch, dev)
             rd4.attn_decode_append(to_dev(q, torch, dev), to_dev(kn, torch, dev), to_dev(vn, torch, dev),
                                    kd, vd, out, r, NH, NKV, HD, 1 / 16, kt, vt, gate=gd)
@@ -122,7 +122,7 @@ def test_draft_then_verify(rd4, orc, dev, kt, vt):
     assert np.array_equal(kd.cpu().numpy(), k_ref) and np.array_equal(vd.cpu().numpy(), v_ref)
     q = orc.randn((D + 1) * NH * HD, 370)
     g = orc.randn((D + 1) * NH * HD, 371)
-    out = torch.empty((D + 1) * NH * HD, device=dev)
+    out = torch.full(((D + 1) * NH * HD,), float("nan"), device=dev)
     gd = to_dev(g, torch, dev)
     rd4.attn_decode_tokens(to_dev(q, torch, dev), kd, vd, out, n0, D + 1, NH, NKV, HD, 1 / 16, kt, vt,
                            gate=gd)
@@ -140,7 +140,7 @@ def test_verify_full_size_q8_0_32k(rd4, orc, dev):
     n, n_tok = 32768, 4
     k, v, kd, vd = _caches(orc, torch, dev, 2, 2, n, 380)
     q = orc.randn(n_tok * NH * HD, 390)
-    out = torch.empty(n_tok * NH * HD, device=dev)
+    out = torch.full((n_tok * NH * HD,), float("nan"), device=dev)
     rd4.attn_decode_tokens(to_dev(q, torch, dev), kd, vd, out, n - n_tok, n_tok, NH, NKV, HD, 1 / 16,
                            2, 2)
     torch.cuda.synchronize()
@@ -183,7 +183,7 @@ def test_layer_verify_step_epilogue_then_tokens(rd4, orc, dev, kt, vt):
                             to_dev(qw, torch, dev), to_dev(kw, torch, dev), eps, n_rot, base,
                             to_dev(pos, torch, dev), n_tok, NH, NKV, HD, q_out, kd, vd, kt, vt,
                             gate_out=g_out, k_out=k_out)
-    out = torch.empty_like(q_out)
+    out = torch.full_like(q_out, float("nan"))  # unwritten elements stay NaN
     rd4.attn_decode_tokens(q_out, kd, vd, out, n0, n_tok, NH, NKV, HD, 1 / 16, kt, vt, gate=g_out)
     torch.cuda.synchronize()
     # oracle pipeline on the host
@@ -211,11 +211,11 @@ def test_tokens_wide_group_takes_per_token_ctas(rd4, orc, dev):
     kd, vd = to_dev(k, torch, dev), to_dev(v, torch, dev)
     q = orc.randn(n_tok * nh * HD, 702)
     qd = to_dev(q, torch, dev)
-    out = torch.empty_like(qd)
+    out = torch.full_like(qd, float("nan"))  # unwritten elements stay NaN
     rd4.attn_decode_tokens(qd, kd, vd, out, n - n_tok, n_tok, nh, nkv, HD, 1 / 16, 3, 3, n_splits=5)
     per = []
     for i in range(n_tok):
-        o = torch.empty(nh * HD, device=dev)
+        o = torch.full((nh * HD,), float("nan"), device=dev)
         rd4.attn_decode(qd[i * nh * HD:(i + 1) * nh * HD].clone(), kd, vd, o, n - n_tok + i, nh, nkv, HD,
                         1 / 16, 3, 3, n_splits=5)
         per.append(o)

@@ -29,7 +29,7 @@ def test_caller_partial_receives_the_records(rd4, orc, dev):
     nbytes = rd4.attn_partial_bytes(NH, HD, S)
     assert nbytes == NH * S * (2 + HD) * 4
     part = torch.full((nbytes // 4 + 64,), float("nan"), dtype=torch.float32, device=dev)
-    out = torch.empty(NH * HD, dtype=torch.float32, device=dev)
+    out = torch.full((NH * HD,), float("nan"), dtype=torch.float32, device=dev)
     rd4.attn_launch_split(to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev), out, part,
                           n - 1, NH, NKV, HD, 1 / 16, 2, 2, S)
     torch.cuda.synchronize()
@@ -55,7 +55,7 @@ def test_two_streams_race_free(rd4, orc, dev, mode):
     # n_splits 2 (the library runs 64, so each stream's own scratch holds them)
     S = 64 if mode == "caller_partial" else 2
     parts = [torch.empty(rd4.attn_partial_bytes(NH, HD, S) // 4, device=dev) for _ in range(2)]
-    outs = [[torch.empty(NH * HD, device=dev) for _ in range(12)] for _ in range(2)]
+    outs = [[torch.full((NH * HD,), float("nan"), device=dev) for _ in range(12)] for _ in range(2)]
     torch.cuda.synchronize()
     for it in range(12):
         for i in range(2):
@@ -82,7 +82,7 @@ def test_split_batch_caller_partial(rd4, orc, dev):
     pos = np.int32([100, 250, 400, 598, 599])
     want = orc.attn_batch(q, k, v, pos, NH, NKV, HD, 1 / 16, 1, 1)
     part = torch.full((ntok * rd4.attn_partial_bytes(NH, HD, S) // 4,), float("nan"), device=dev)
-    out = torch.empty(ntok * NH * HD, device=dev)
+    out = torch.full((ntok * NH * HD,), float("nan"), device=dev)
     rd4.attn_split_batch(to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev), out,
                          to_dev(pos, torch, dev), NH, NKV, HD, 1 / 16, 1, 1, S, partial=part)
     torch.cuda.synchronize()
@@ -103,7 +103,7 @@ def test_split_batch_token_chunks(rd4, orc, dev, kt):
     q = orc.randn(ntok * NH * HD, 92).reshape(ntok, NH, HD)
     pos = np.int32(np.random.default_rng(3).integers(100, n, ntok))
     want = orc.attn_batch(q, k, v, pos, NH, NKV, HD, 1 / 16, kt, kt, threads=8)
-    out = torch.empty(ntok * NH * HD, device=dev)
+    out = torch.full((ntok * NH * HD,), float("nan"), device=dev)
     rd4.attn_split_batch(to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev), out,
                          to_dev(pos, torch, dev), NH, NKV, HD, 1 / 16, kt, kt, S)
     torch.cuda.synchronize()

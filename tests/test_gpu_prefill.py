@@ -23,7 +23,7 @@ def test_prefill_small(rd4, orc, dev, q_f16):
     att = orc.attn_batch(q, k, v, pos, nh, nkv, hd, 1 / 16, 1, 1)
     gs, want = orc.sigmoid_gate(g, att.ravel())
     qd = to_dev(q.astype(np.float16) if q_f16 else q, torch, dev)
-    out = torch.empty(nq * nh * hd, dtype=torch.float32, device=dev)
+    out = torch.full((nq * nh * hd,), float("nan"), dtype=torch.float32, device=dev)
     gd = to_dev(g, torch, dev)
     rd4.prefill(qd, to_dev(k, torch, dev), to_dev(v, torch, dev), out, pos0, nh, nkv, hd, 1 / 16,
                 1, 1, gate=gd)
@@ -68,7 +68,7 @@ def test_prefill_shapes(rd4, orc, dev, nh, nkv, pos0, nq, q_f16, gated):
     if gated:
         _, want = orc.sigmoid_gate(g, want)
     qd = to_dev(q.astype(np.float16) if q_f16 else q, torch, dev)
-    out = torch.empty(nq * nh * hd, dtype=torch.float32, device=dev)
+    out = torch.full((nq * nh * hd,), float("nan"), dtype=torch.float32, device=dev)
     rd4.prefill(qd, to_dev(k, torch, dev), to_dev(v, torch, dev), out, pos0, nh, nkv, hd, 1 / 16, 1, 1,
                 gate=to_dev(g, torch, dev) if gated else None)
     check_close(out.cpu().numpy(), want, "prefill %d/%d pos0 %d n %d" % (nh, nkv, pos0, nq))
@@ -84,7 +84,7 @@ def test_prefill_config5_sampled_rows(rd4, orc, dev):
     v = orc.store_rows(1, orc.randn(n * nkv * hd, 22))
     q = orc.randn(nq * nh * hd, 23).reshape(nq, nh, hd).astype(np.float16)
     g = orc.randn(nq * nh * hd, 24).reshape(nq, nh, hd)
-    out = torch.empty((nq, nh, hd), dtype=torch.float32, device=dev)
+    out = torch.full((nq, nh, hd), float("nan"), dtype=torch.float32, device=dev)
     gd = to_dev(g, torch, dev)
     rd4.prefill(to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev), out, pos0, nh, nkv,
                 hd, 1 / 16, 1, 1, gate=gd)
@@ -157,7 +157,7 @@ def test_prefill_append_rejects_overlap(rd4, orc, dev):
     k = torch.zeros(n * nkv * rb, dtype=torch.uint8, device=dev)
     v = torch.zeros_like(k)
     q = torch.zeros(nq * nh * hd, dtype=torch.float16, device=dev).reshape(nq, nh, hd)
-    out = torch.empty(nq * nh * hd, dtype=torch.float32, device=dev)
+    out = torch.full((nq * nh * hd,), float("nan"), dtype=torch.float32, device=dev)
     src = torch.zeros(nq * nkv * hd, dtype=torch.float32, device=dev)
     with pytest.raises(rd4.Rd4Error):
         rd4.prefill_append(q, k, v, out, pos0, nh, nkv, hd, 1 / 16, 1, 1, src, src,
@@ -187,7 +187,7 @@ def test_prefill_append_config5_full(rd4, orc, dev, monkeypatch):
     kq8 = torch.zeros(n * nkv * rb, dtype=torch.uint8, device=dev)
     vq8 = torch.zeros_like(kq8)
     qd, kd, vd = to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev)
-    out = torch.empty((nq, nh, hd), dtype=torch.float32, device=dev)
+    out = torch.full((nq, nh, hd), float("nan"), dtype=torch.float32, device=dev)
     gd = to_dev(g, torch, dev)
     off = pos0 * nkv * rb
     rd4.prefill_append(qd, kd, vd, out, pos0, nh, nkv, hd, 1 / 16, 1, 1, to_dev(knew, torch, dev),
@@ -244,7 +244,7 @@ k = orc.store_rows(1, orc.randn(n * nkv * hd, 41))
 v = orc.store_rows(1, orc.randn(n * nkv * hd, 42))
 q = orc.randn(nq * nh * hd, 43).reshape(nq, nh, hd).astype(np.float16)
 g = orc.randn(nq * nh * hd, 44).reshape(nq, nh, hd)
-out = torch.empty((nq, nh, hd), dtype=torch.float32, device=dev)
+out = torch.full((nq, nh, hd), float("nan"), dtype=torch.float32, device=dev)
 gd = to_dev(g, torch, dev)
 rd4.prefill(to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev), out, pos0, nh, nkv, hd,
             1 / 16, 1, 1, gate=gd)
@@ -260,3 +260,52 @@ print("ok")
     r = subprocess.run([sys.executable, "-c", code, shape], cwd=root, env=env, capture_output=True,
                        text=True, timeout=180)
     assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
+@pytest.mark.parametrize("split", ["8x512", "1+3+4"])
+def test_prefill_chunked_equals_one_call(rd4, orc, dev, split):
+    """Chunked prefill gives the same bits as one call over the whole chunk: the
+    reference requires chunks 1+3+4 to equal one pass (check_kvctx_gpu.hip:109-163),
+    and its engine sends a 4096-token prompt as 8 calls of 512 queries
+    (graph.cuh:1890-1939, fa2_prefill_usable's n_q == 512, attn_fa2.cuh:192-207).
+    Each query row's arithmetic depends only on its own keys: key blocks past a
+    row's causal limit are masked to exact zeros, so outputs, gate and the
+    appended q8_0 bytes must match bit for bit."""
+    import torch
+    nh, nkv, hd = 24, 4, 256
+    if split == "8x512":
+        pos0, sizes = 4096, [512] * 8
+    else:
+        pos0, sizes = 1000, [1, 3, 4]
+    nq = sum(sizes)
+    n = pos0 + nq
+    k = orc.store_rows(1, orc.randn(n * nkv * hd, 91))
+    v = orc.store_rows(1, orc.randn(n * nkv * hd, 92))
+    q = orc.randn(nq * nh * hd, 93).reshape(nq, nh, hd).astype(np.float16)
+    g = orc.randn(nq * nh * hd, 94).reshape(nq, nh, hd)
+    knew = orc.randn(nq * nkv * hd, 95).reshape(nq, nkv, hd)
+    vnew = orc.randn(nq * nkv * hd, 96).reshape(nq, nkv, hd)
+    rb = rd4.kv_row_bytes(2, hd)
+    qd, kd, vd = to_dev(q, torch, dev), to_dev(k, torch, dev), to_dev(v, torch, dev)
+    kn, vn = to_dev(knew, torch, dev), to_dev(vnew, torch, dev)
+    res = []
+    for chunks in ([nq], sizes):
+        out = torch.full((nq, nh, hd), float("nan"), dtype=torch.float32, device=dev)
+        gd = to_dev(g, torch, dev)
+        kq8 = torch.zeros(nq * nkv * rb, dtype=torch.uint8, device=dev)
+        vq8 = torch.zeros_like(kq8)
+        r0 = 0
+        for c in chunks:
+            rd4.prefill_append(qd[r0:r0 + c], kd, vd, out[r0:r0 + c], pos0 + r0, nh, nkv, hd, 1 / 16, 1, 1,
+                               kn[r0:r0 + c], vn[r0:r0 + c], kq8[r0 * nkv * rb:], vq8[r0 * nkv * rb:], 2,
+                               gate=gd[r0:r0 + c])
+            r0 += c
+        torch.cuda.synchronize()
+        res.append([t.cpu().numpy() for t in (out, gd, kq8, vq8)])
+    for a, b, what in zip(res[0], res[1], ("out", "gate", "k q8_0", "v q8_0")):
+        assert np.array_equal(a, b), "%s: chunked %s differs from one call" % (what, split)
+    # and the one-call result itself against the oracle on its last rows
+    rows = np.int32([nq - 1, nq - 2, 0])
+    want = orc.attn_batch(q[rows].astype(np.float32), k, v, pos0 + rows, nh, nkv, hd, 1 / 16, 1, 1, threads=8)
+    _, want = orc.sigmoid_gate(g[rows], want)
+    check_close(res[0][0][rows].ravel(), want, "chunked prefill rows vs oracle")
