@@ -63,6 +63,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #ifndef RD4_DEC_AUX
 #define RD4_DEC_AUX 0
 #endif
+// The ring's next tile is requested after the current tile's QK product
+// instead of before its wait: under a chip-wide burst of requests the DMA
+// instructions hold the issuing wave (0.4-1.3 us per tile in a timeline of
+// every wave), and there the hold no longer delays a tile that has landed.
+#ifndef RD4_DEC_LATE
+#define RD4_DEC_LATE 1
+#endif
 constexpr int kHD = 256;     // head_dim of this kernel
 constexpr int kRowPad = kHD + 4;  // LDS row stride (floats) of per-head rows: spreads banks
 constexpr int kTile = 16;    // keys per wave tile
@@ -1215,6 +1222,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   // state of the current tile, shared by the exp/PV step and the rescale
   float sc[4];
   const uint8_t *vl = nullptr;
+  int i = 0;  // this wave's tile being processed
   auto finish = [&]() __attribute__((always_inline)) {
     float psum = 0.0f;
     // a row that has seen no key yet (pair mode, a split holding only the
@@ -1349,22 +1357,27 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
   // copies all 64 back on every tile.)
   RD4_TP();
   if (RD4_DEC_KNOBS && (a.dbg & 16384)) return;  // profiling: up to the tile loop
-  int i = 0;
   for (;;) {
     bool rescale_due = false;
     for (; i < my_tiles; ++i) {
       RD4_TP();
       const int j_tile = j_begin + tile_of(i) * j_step;
       const int nk = min(kTile, j_end - j_tile);
-      if (next_issue <= i + R - 1 && next_issue < my_tiles) {
+      // the next tiles go out here, or with RD4_DEC_LATE after this tile's QK
+      // product (then only a tile this iteration needs itself is issued here)
+      const int issue_to = RD4_DEC_LATE ? i : i + R - 1;
+      if (next_issue <= issue_to && next_issue < my_tiles) {
         // the stage being refilled was read by the previous iteration: those reads are done
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         do {
           issue(next_issue++);
-        } while (next_issue <= i + R - 1 && next_issue < my_tiles);
+        } while (next_issue <= issue_to && next_issue < my_tiles);
       }
+#if RD4_DEC_TRACE >= 2
+      RD4_TP();
+#endif
       // tile i is complete once at most the loads of the tiles issued after it remain
-      const int after = min(R - 1, my_tiles - 1 - i);
+      const int after = next_issue - 1 - i;
       if (after >= 3) wait_vm<3 * NI>();
       else if (after == 2) wait_vm<2 * NI>();
       else if (after == 1) wait_vm<NI>();
@@ -1496,6 +1509,12 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
             }
           }
         }
+      }
+      if (RD4_DEC_LATE && next_issue <= i + R - 1 && next_issue < my_tiles) {
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        do {
+          issue(next_issue++);
+        } while (next_issue <= i + R - 1 && next_issue < my_tiles);
       }
       RD4_TP();
       // Rows n and n^8 are the hi and lo halves of the same head. (A DPP
