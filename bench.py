@@ -341,9 +341,19 @@ def read_ceiling(rd4, args, torch, steps=None):
     gbs = nbytes * args.layers / (wall_ms * 1e-3) / 1e9
     del bufs
     torch.cuda.empty_cache()
+    # the same graph of launches over 4 KiB buffers: what a launch costs in a
+    # replayed graph when it reads (almost) nothing
+    tiny = [torch.full((4096,), l, dtype=torch.uint8, device="cuda") for l in range(args.layers)]
+
+    def step0():
+        for b in tiny:
+            rd4.read_probe(b, sink)
+    run0 = as_graph(torch, step0) or step0
+    floor_ms, _ = measure(torch, run0, run0, steps or args.steps, args.warmup)
     return {"bytes_per_launch": nbytes, "launches_per_step": args.layers,
             "us_per_launch": round(wall_ms * 1e3 / args.layers, 3), "GB/s": round(gbs, 1),
-            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "launch_floor_us": round(floor_ms * 1e3 / args.layers, 3)}
 
 
 def build_workload(torch, rd4, name, args):

@@ -30,6 +30,7 @@
 //   * causal masking only in blocks that cross a row's limit (a wave-uniform
 //     branch).
 // Row blocks are scheduled heaviest (latest queries) first.
+#include <algorithm>
 #include <cstdlib>
 
 #include "kv_quant.hpp"
@@ -231,7 +232,10 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   // in turn (heaviest first), so an XCD's L2 serves one kv head whose CTAs
   // sweep the same keys at about the same time.
   const int total = n_rb * p.n_head_kv;
-  const int L = blockIdx.x;
+  // key split of this CTA: the splits' grids follow one another, so workgroup
+  // L of a split still runs on XCD L % 8 (total is a multiple of 8 there)
+  const int ksp = p.n_ksplit > 1 ? (int)blockIdx.x / total : 0;
+  const int L = p.n_ksplit > 1 ? (int)blockIdx.x - ksp * total : (int)blockIdx.x;
   int kvh, rbp;
   if (8 % p.n_head_kv == 0 && total % 8 == 0) {
     const int X = 8 / p.n_head_kv, xcd = L % 8, j = L / 8;
@@ -247,10 +251,10 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   // Fused append: the chunk's new K and V rows (2 * n_q * n_head_kv of them) are
   // spread over the CTAs, one wave per row, 8 lanes per 32-value block, with the
   // quantizer of kv_store_row_launch; the attention below reads other rows.
-  if (p.app_k) {
+  if (p.app_k && ksp == 0) {  // (the first split's CTAs)
     const int nrow = p.n_q * p.n_head_kv, total_rows = 2 * nrow;
     const int rb_bytes = (int)row_bytes(p.app_type, kHD);
-    for (int R = (int)blockIdx.x * W + w; R < total_rows; R += (int)gridDim.x * W) {
+    for (int R = L * W + w; R < total_rows; R += total * W) {
       const bool isv = R >= nrow;
       const int rr = isv ? R - nrow : R;
       const float4 x4 = *(const float4 *)((isv ? p.app_v_src : p.app_k_src) + (int64_t)rr * kHD + 4 * lane);
@@ -285,6 +289,9 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
     kend = __builtin_amdgcn_readfirstlane(lim);
   }
   const int n_blocks = (RD4_PF_KNOB & 64) ? 0 : (kend + kBN) / kBN;
+  // this CTA's blocks b0 .. b0 + nbk - 1 (all of them when the keys are not split)
+  const int b0 = p.n_ksplit > 1 ? ksp * p.ksplit_blocks : 0;
+  const int nbk = p.n_ksplit > 1 ? max(0, min(n_blocks, b0 + p.ksplit_blocks) - b0) : n_blocks;
 
   const int64_t kvstride = (int64_t)p.n_head_kv * kHD * 2;  // bytes between consecutive keys
   const uint8_t *kbase = p.k + (int64_t)kvh * kHD * 2;
@@ -415,19 +422,20 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
 
   // Issue order: K0 V0 K1, then in block j: V(j+1) at the top, K(j+2) after
   // the QK^T phase.
-  if (n_blocks > 0) {
-    issue_k(0, 0);
-    issue_v(0, 0);
+  if (nbk > 0) {
+    issue_k(b0, 0);
+    issue_v(b0, 0);
   }
-  if (n_blocks > 1) issue_k(1, 1);
+  if (nbk > 1) issue_k(b0 + 1, 1);
   int ks = 0;  // K stage of the current block (blk % 3)
 #if RD4_PF_PROBE
   float pr_a = 0.f, pr_b = 1.f;
   floatx4 pr_c = {0.f, 0.f, 0.f, 0.f};
   u32x4 pr_d = {0, 0, 0, 0};
 #endif
-  for (int blk = 0; blk < n_blocks; ++blk) {
-    const int vs = blk & 1;
+  for (int bi = 0; bi < nbk; ++bi) {
+    const int blk = b0 + bi;
+    const int vs = bi & 1;
     // every DMA this wave issued has landed: K(j), V(j) and also K(j+1), which
     // was requested a block earlier and has landed by now (waiting for it costs
     // nothing measurable). A partial count would assume that the DMA completes
@@ -438,7 +446,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
     // barrier on LDS only, in asm)
 #ifndef RD4_PF_FULLBAR
     if (!(RD4_PF_KNOB & 16)) __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (blk < 12) RD4_PFTP(5 * blk + 1);
+    if (bi < 12) RD4_PFTP(5 * bi + 1);
 #else
     __syncthreads();
 #endif
@@ -446,8 +454,8 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
     // DMA issue points (RD4_PF_DMAPOS, default 1): 0 both at the block top, 1 K(blk + 2)
     // after the QK^T phase, 3 both after it
     if (!(RD4_PF_KNOB & 8)) {
-      if (RD4_PF_DMAPOS != 3 && blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
-      if (RD4_PF_DMAPOS == 0 && blk + 2 < n_blocks) issue_k(blk + 2, ks2);
+      if (RD4_PF_DMAPOS != 3 && bi + 1 < nbk) issue_v(blk + 1, vs ^ 1);
+      if (RD4_PF_DMAPOS == 0 && bi + 2 < nbk) issue_k(blk + 2, ks2);
     }
     const uint8_t *kd = smem + ks * kKBytes;
     const uint8_t *vd = smem + (kKStages + vs) * kKBytes;
@@ -486,7 +494,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
                     : __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[sl][f & 7], s[sl][kt], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (blk < 12) RD4_PFTP(5 * blk + 2);
+    if (bi < 12) RD4_PFTP(5 * bi + 2);
     half8 vb[kPVD][2];
     // step t: key group kg = t / 8, dim tiles 2(t % 8), +1
     auto read_vb = [&](int buf, int t) {
@@ -509,11 +517,11 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       __builtin_amdgcn_sched_barrier(0);
     }
     if (!(RD4_PF_KNOB & 8) && RD4_PF_DMAPOS != 0) {
-      if (RD4_PF_DMAPOS == 3 && blk + 1 < n_blocks) issue_v(blk + 1, vs ^ 1);
-      if (blk + 2 < n_blocks) issue_k(blk + 2, ks2);
+      if (RD4_PF_DMAPOS == 3 && bi + 1 < nbk) issue_v(blk + 1, vs ^ 1);
+      if (bi + 2 < nbk) issue_k(blk + 2, ks2);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (blk < 12) RD4_PFTP(5 * blk + 3);
+    if (bi < 12) RD4_PFTP(5 * bi + 3);
     // ---- online softmax per slab: lane = row n, keys 16kt + 4g + i
     half8 pf[NSL][2];
     if (RD4_PF_KNOB & 4) {
@@ -577,7 +585,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
 #pragma unroll
         for (int i = 0; i < 8; ++i) pf[sl][kg][i] = (_Float16)s[sl][2 * kg + (i >> 2)][i & 3];
     }
-    if (blk < 12) RD4_PFTP(5 * blk + 4);
+    if (bi < 12) RD4_PFTP(5 * bi + 4);
     // ---- O^T += V^T P^T: A = 16 dims x 32 keys of V (k-slot 8g + j is key
     // 32kg + 16(j/4) + 4g + j%4, as in pf), two transposing loads per operand;
     // the next two dim tiles' operands are read while the current ones run.
@@ -599,7 +607,7 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
       }
       if (RD4_PF_SB & 2) __builtin_amdgcn_sched_barrier(0);
     }
-    if (blk < 12) RD4_PFTP(5 * blk + 5);
+    if (bi < 12) RD4_PFTP(5 * bi + 5);
 #if RD4_PF_PROBE
     // sensitivity probes (diagnostic builds only): extra independent work per block
     if (RD4_PF_PROBE & 1)
@@ -614,7 +622,8 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   if (p.scale == 12345.0f) p.out[tid] = pr_a + pr_b + pr_c[0] + (float)pr_d[0];
 #endif
 
-  // ---- epilogue: l over the 4 key groups, normalize, gate, store
+  // ---- epilogue: l over the 4 key groups, normalize, gate, store (or, for a
+  // key split, the unnormalized record)
 #pragma unroll
   for (int sl = 0; sl < NSL; ++sl) {
     float L = l_run[sl];
@@ -623,6 +632,15 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
     const int row = r0 + kRowsWT * w + 16 * sl + n;
     if (row >= n_rows) continue;
     const int q = row / grp, head = kvh * grp + row % grp;
+    if (p.n_ksplit > 1) {
+      const int64_t nr = (int64_t)p.n_q * p.n_head, rr = (int64_t)ksp * nr + (int64_t)q * p.n_head + head;
+      float *rec = p.part + rr * kHD;
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt)
+        *(floatx4 *)(rec + 16 * dt + 4 * g) = o[sl][dt];
+      if (g == 0) *(float2 *)(p.part + (int64_t)p.n_ksplit * nr * kHD + 2 * rr) = make_float2(m_run[sl], L);
+      continue;
+    }
     const float inv = (m_run[sl] == -INFINITY || !(L > 0.0f)) ? 0.0f : 1.0f / L;
     const int64_t ob = ((int64_t)q * p.n_head + head) * kHD;
 #pragma unroll
@@ -644,10 +662,75 @@ __global__ __launch_bounds__(64 * W, 1) void prefill_mfma_kernel(PrefillArgs p) 
   }
 }
 
+// Fold of the key splits' records (the LSE merge of the split decode, exp2
+// domain), then the gate and the store of the unsplit epilogue: one wave per
+// (query, head) row, 4 dims per lane.
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nr = (int64_t)p.n_q * p.n_head;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= nr) return;
+  const int S = p.n_ksplit;
+  const float *ml = p.part + (int64_t)S * nr * kHD;
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * (s * nr + row)]);
+  float L = 0.0f;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < S; ++s) {
+    const float2 r = *(const float2 *)(ml + 2 * (s * nr + row));
+    if (r.x == -INFINITY) continue;  // a split with no key of this row
+    const float wgt = __builtin_amdgcn_exp2f(r.x - M);
+    L = fmaf(wgt, r.y, L);
+    const floatx4 v = *(const floatx4 *)(p.part + (s * nr + row) * kHD + 4 * lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = fmaf(wgt, v[i], acc[i]);
+  }
+  const float inv = (M == -INFINITY || !(L > 0.0f)) ? 0.0f : 1.0f / L;
+  const int64_t ob = row * kHD + 4 * lane;
+  float v[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+  if (p.gate) {
+    float4 gv = *(const float4 *)(p.gate + ob);
+    float gs[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      gs[i] = 1.0f / (1.0f + expf(-gs[i]));
+      v[i] *= gs[i];
+    }
+    *(float4 *)(p.gate + ob) = make_float4(gs[0], gs[1], gs[2], gs[3]);
+  }
+  *(float4 *)(p.out + ob) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
 bool prefill_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim) {
   const char *e = std::getenv("RD4_PREFILL_GENERIC");
   if (e && std::atoi(e) != 0) return false;
   return kt == F16 && vt == F16 && head_dim == kHD && n_head_kv > 0 && n_head % n_head_kv == 0;
+}
+
+// Key splits the MFMA kernel wants for this call: when its row blocks leave
+// CUs idle (the reference engine's 512-query chunks: 64 CTAs on 256 CUs),
+// about one CTA per CU, at most 16 and at most one per key block.
+// RD4_PREFILL_KSPLIT forces a count (1: never split).
+int prefill_ksplits(const PrefillArgs &p) {
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    return n;
+  }();
+  static const int env = [] {
+    const char *e = std::getenv("RD4_PREFILL_KSPLIT");
+    return e ? std::atoi(e) : 0;
+  }();
+  const int grp = p.n_head / p.n_head_kv;
+  const int total = (p.n_q * grp + 191) / 192 * p.n_head_kv;  // the default 192-row CTAs
+  const int max_blocks = (p.kmax + kBN) / kBN;
+  int s = env > 0 ? env : (total % 8 == 0 && 2 * total <= cus) ? cus / total : 1;
+  return std::max(1, std::min(s, std::min(max_blocks, 16)));
+}
+int64_t prefill_part_floats(const PrefillArgs &p, int splits) {
+  return (int64_t)splits * p.n_q * p.n_head * (kHD + 2);
 }
 
 hipError_t prefill_mfma_launch(const PrefillArgs &p, hipStream_t st) {
@@ -658,15 +741,34 @@ hipError_t prefill_mfma_launch(const PrefillArgs &p, hipStream_t st) {
   const int grp = p.n_head / p.n_head_kv;
   const int bm = shape == 2 ? 256 : shape == 0 ? 192 : 128;  // rows per CTA
   const int n_rb = (p.n_q * grp + bm - 1) / bm;
-  dim3 grid((unsigned)(n_rb * p.n_head_kv));
+  const int total = n_rb * p.n_head_kv;
+  // Key splits when the row blocks alone leave CUs idle (the reference
+  // engine's 512-query chunks: 64 CTAs on 256 CUs): enough splits of equal
+  // block counts to give about one CTA per CU, if the records fit the scratch.
+  PrefillArgs q = p;
+  q.n_ksplit = 1;
+  q.ksplit_blocks = 0;
+  const int s = prefill_ksplits(p);
+  if (s > 1 && p.part && prefill_part_floats(p, s) <= p.part_floats) {
+    const int max_blocks = (p.kmax + kBN) / kBN;
+    q.ksplit_blocks = (max_blocks + s - 1) / s;
+    q.n_ksplit = (max_blocks + q.ksplit_blocks - 1) / q.ksplit_blocks;
+  }
+  dim3 grid((unsigned)(total * q.n_ksplit));
   if (shape == 1)  // 4 waves x 32 rows (one wave per SIMD)
-    hipLaunchKernelGGL((prefill_mfma_kernel<4, 2>), grid, dim3(256), (size_t)kLdsBytes, st, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<4, 2>), grid, dim3(256), (size_t)kLdsBytes, st, q);
   else if (shape == 2)  // 8 waves x 32 rows (two waves per SIMD)
-    hipLaunchKernelGGL((prefill_mfma_kernel<8, 2>), grid, dim3(512), (size_t)kLdsBytes, st, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<8, 2>), grid, dim3(512), (size_t)kLdsBytes, st, q);
   else if (shape == 3)  // 8 waves x 16 rows (two waves per SIMD)
-    hipLaunchKernelGGL((prefill_mfma_kernel<8, 1>), grid, dim3(512), (size_t)kLdsBytes, st, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<8, 1>), grid, dim3(512), (size_t)kLdsBytes, st, q);
   else  // 12 waves x 16 rows (three waves per SIMD)
-    hipLaunchKernelGGL((prefill_mfma_kernel<12, 1>), grid, dim3(768), (size_t)kLdsBytes, st, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<12, 1>), grid, dim3(768), (size_t)kLdsBytes, st, q);
+  if (q.n_ksplit > 1) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t rows = (int64_t)p.n_q * p.n_head;
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, q);
+  }
   return hipGetLastError();
 }
 

@@ -541,6 +541,19 @@ int rd4_attn_split_batch_launch(const float *q, const void *k, const void *v, fl
                   vt, n_splits, (hipStream_t)stream, nullptr, nullptr, 0, partial, n_splits);
 }
 
+// The MFMA prefill's key splits write records to the stream's library
+// scratch; a call that would split gets it here (without it, no split).
+void prefill_part(PrefillArgs &p, int kt, int vt, hipStream_t st) {
+  const uintptr_t al = (uintptr_t)p.q | (uintptr_t)p.k | (uintptr_t)p.v | (uintptr_t)p.out | (uintptr_t)p.gate;
+  if ((al & 15) || !prefill_mfma_supported(kt, vt, p.n_head, p.n_head_kv, p.head_dim)) return;
+  const int s = prefill_ksplits(p);
+  Scratch *sc = nullptr;
+  if (s > 1 && prefill_part_floats(p, s) <= kPartialFloats && get_scratch(st, &sc) == RD4_OK) {
+    p.part = sc->partial_c;
+    p.part_floats = kPartialFloats;
+  }
+}
+
 int rd4_fa2_prefill_usable(int kt, int vt, int n_q, int pos0, int n_head, int n_head_kv,
                            int head_dim) {
   const char *e = std::getenv("RD_GFX12_FA2_PREFILL");
@@ -572,6 +585,7 @@ int rd4_fa2_prefill_launch(const float *q, const void *k, const void *v, float *
   p.n_head_kv = n_head_kv;
   p.head_dim = head_dim;
   p.scale = scale;
+  prefill_part(p, RD4_KV_F16, RD4_KV_F16, (hipStream_t)stream);
   return launched(prefill_launch(RD4_KV_F16, RD4_KV_F16, p, (hipStream_t)stream), "prefill");
 }
 
@@ -596,6 +610,7 @@ int rd4_prefill(const void *q, int q_f16, const void *k, const void *v, float *o
   p.n_head_kv = n_head_kv;
   p.head_dim = head_dim;
   p.scale = scale;
+  prefill_part(p, kt, vt, (hipStream_t)stream);
   return launched(prefill_launch(kt, vt, p, (hipStream_t)stream), "prefill");
 }
 
@@ -657,6 +672,7 @@ int rd4_prefill_append(const void *q, int q_f16, const void *k, const void *v, f
   p.app_k = (uint8_t *)k_dst;
   p.app_v = (uint8_t *)v_dst;
   p.app_type = dst_type;
+  prefill_part(p, kt, vt, (hipStream_t)stream);
   return launched(prefill_launch(kt, vt, p, (hipStream_t)stream), "prefill");
 }
 

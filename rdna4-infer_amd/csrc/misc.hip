@@ -68,24 +68,27 @@ hipError_t fill_u32_launch(uint32_t *p, int64_t n, uint32_t v, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Streaming read of n16 16-byte words (bench calibration: the practical HBM
-// read rate of one launch). Grid-stride, U independent 16-byte loads in flight
-// per thread; the xor of everything is written only if it hits an unlikely
-// value, so the loads cannot be removed.
+// Streaming-read probe: the bench's measure of what a launch that only reads
+// the decode step's bytes reaches. Each CTA reads one contiguous chunk of the
+// buffer (as a decode split does), U 16-byte loads per lane in flight; the xor
+// of everything is written only if it hits an unlikely value, so the loads
+// cannot be removed.
 template <int U>
 __global__ __launch_bounds__(1024) void read_probe_kernel(const uint4 *__restrict__ p, int64_t n16,
                                                           uint32_t *__restrict__ sink) {
   uint32_t acc = 0;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i + (U - 1) * stride < n16; i += U * stride) {
+  const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+  const int64_t lo = per * blockIdx.x, hi = min(n16, lo + per);
+  const int T = blockDim.x;
+  int64_t i = lo + threadIdx.x;
+  for (; i + (U - 1) * T < hi; i += U * T) {
     uint4 x[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) x[u] = p[i + u * stride];
+    for (int u = 0; u < U; ++u) x[u] = p[i + u * T];
 #pragma unroll
     for (int u = 0; u < U; ++u) acc ^= x[u].x ^ x[u].y ^ x[u].z ^ x[u].w;
   }
-  for (; i < n16; i += stride) {
+  for (; i < hi; i += T) {
     const uint4 a = p[i];
     acc ^= a.x ^ a.y ^ a.z ^ a.w;
   }
@@ -101,9 +104,10 @@ hipError_t read_probe_launch(const void *p, int64_t bytes, uint32_t *sink, hipSt
     init = true;
     if (const char *e = std::getenv("RD4_PROBE")) std::sscanf(e, "%d,%d,%d", &shape[0], &shape[1], &shape[2]);
   }
-  // default: the fastest shape measured on MI355X for a 71 MB read (larger
-  // grids and more loads in flight per thread were slower)
-  const int nb = shape[0] > 0 ? shape[0] : 256, nt = shape[1] > 0 ? shape[1] : 512, u = shape[2] > 0 ? shape[2] : 4;
+  // default: the fastest shape measured on MI355X for a 71 MB read among
+  // 256-1024 CTAs x 256-1024 threads x 4-16 loads in flight per lane (1024 x
+  // 512 x 4: 12.97 us per 71.3 MB launch, graph-replayed; 512 x 512 x 8 13.2 us)
+  const int nb = shape[0] > 0 ? shape[0] : 1024, nt = shape[1] > 0 ? shape[1] : 512, u = shape[2] > 0 ? shape[2] : 4;
   const uint4 *q = (const uint4 *)p;
   if (u == 4) hipLaunchKernelGGL(read_probe_kernel<4>, dim3(nb), dim3(nt), 0, st, q, bytes / 16, sink);
   else if (u == 16) hipLaunchKernelGGL(read_probe_kernel<16>, dim3(nb), dim3(nt), 0, st, q, bytes / 16, sink);

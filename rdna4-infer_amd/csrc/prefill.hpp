@@ -22,6 +22,15 @@ struct PrefillArgs {
   const float *app_k_src, *app_v_src;
   uint8_t *app_k, *app_v;
   int app_type;
+  // Key splits (filled by prefill_mfma_launch): with n_ksplit > 1 CTA split s
+  // takes the key blocks [s * ksplit_blocks, (s + 1) * ksplit_blocks) of its
+  // rows and writes unnormalized records to part (O: [split][q * n_head +
+  // head][hd], then (m, l): [split][q * n_head + head][2]); a merge launch
+  // folds them. part (part_floats floats, library scratch) may be null: then
+  // the kernel never splits.
+  int n_ksplit, ksplit_blocks;
+  float *part;
+  int64_t part_floats;
 };
 
 bool prefill_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim);
@@ -29,6 +38,10 @@ hipError_t prefill_launch(int kt, int vt, const PrefillArgs &p, hipStream_t st);
 
 bool prefill_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim);
 hipError_t prefill_mfma_launch(const PrefillArgs &p, hipStream_t st);
+// Key splits the MFMA kernel would run for p (1: none) and the scratch floats
+// their records take; the caller passes the scratch in p.part.
+int prefill_ksplits(const PrefillArgs &p);
+int64_t prefill_part_floats(const PrefillArgs &p, int splits);
 
 bool decode_mfma_supported(int kt, int vt, int n_head, int n_head_kv, int head_dim);
 hipError_t decode_mfma_launch(int kt, int vt, const AttnArgs &a, int n_tok, hipStream_t st);
