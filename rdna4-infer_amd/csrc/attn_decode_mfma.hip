@@ -75,7 +75,13 @@ constexpr int kRowPad = kHD + 4;  // LDS row stride (floats) of per-head rows: s
 constexpr int kTile = 16;    // keys per wave tile
 constexpr int kG = 8;        // query heads per CTA (MFMA rows 0-7 hi, 8-15 lo)
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kQiBytes = 16 * kHD + 16 * 8 * 4;  // int8 query rows [16][8 blocks][32] + scales [16][8]
+// int8 query image (q8_0 K): rows [16][8 blocks][32] padded to kQiRow bytes,
+// then scales [16][8] padded to kSqRow floats per row. The padding spreads the
+// 16 rows read by one lane group over distinct LDS banks (unpadded, the 256-byte
+// rows put all 16 on one bank pair: 5.1e5 conflict cycles per launch, 0.45 us
+// of the q8_0 32K step).
+constexpr int kQiRow = kHD + 16, kSqRow = 12;
+constexpr int kQiBytes = 16 * kQiRow + 16 * kSqRow * 4;
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ void wave_sync() {
@@ -1094,7 +1100,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
     // remainder on s_hi / 254. The int8 image lies past the query rows, so no
     // barrier is needed before it.
     uint8_t *qi = q_lds + kG * (kHD * 4 + 16) + 256;  // [16 rows][8 blocks][32 slots]
-    float *sq = (float *)(qi + 16 * kHD);              // [16 rows][8 blocks] scales (with scale * log2 e)
+    float *sq = (float *)(qi + 16 * kQiRow);           // [16 rows][8 blocks] scales (with scale * log2 e)
 #pragma unroll
     for (int m = 0; m < 8 / kWaves; ++m) {
       const int r = w + kWaves * m;
@@ -1120,7 +1126,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       // inverse of k_dim<Q8_0>): odd blocks e (one aligned word); even blocks
       // e - 2 for 2 <= e < 30, 28 + e below, e above (two aligned 16-bit pairs)
       const int b = lane >> 3, e0 = 4 * (lane & 7);
-      uint8_t *hrow = qi + (r * 8 + b) * 32, *lrow = qi + ((r + 8) * 8 + b) * 32;
+      uint8_t *hrow = qi + r * kQiRow + b * 32, *lrow = qi + (r + 8) * kQiRow + b * 32;
       if (b & 1) {
         *(uint32_t *)(hrow + e0) = bh[0] | bh[1] << 8 | bh[2] << 16 | bh[3] << 24;
         *(uint32_t *)(lrow + e0) = bl[0] | bl[1] << 8 | bl[2] << 16 | bl[3] << 24;
@@ -1132,12 +1138,12 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
         *(uint16_t *)(lrow + s23) = (uint16_t)(bl[2] | bl[3] << 8);
       }
       if ((lane & 7) == 0) {
-        sq[r * 8 + b] = s_hi * a.scale * kLog2e;
-        sq[(r + 8) * 8 + b] = s_lo * a.scale * kLog2e;
+        sq[r * kSqRow + b] = s_hi * a.scale * kLog2e;
+        sq[(r + 8) * kSqRow + b] = s_lo * a.scale * kLog2e;
       }
     }
     lds_barrier();
-    read_qop<kSqReg>(qi + n * 256 + 8 * g, sq + n * 8, qop, sqb);
+    read_qop<kSqReg>(qi + n * kQiRow + 8 * g, sq + n * kSqRow, qop, sqb);
     }
   } else {
     const int hh = n & 7;
@@ -1448,7 +1454,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
             // block scales are read here)
             k_words_q8(krow, g, kw, ke);
             floatx4 s0, s1;
-            tbl_read8_q2(dk_t + 4 * g, (const float *)(q_lds + kG * (kHD * 4 + 16) + 256 + 16 * kHD) + 8 * n,
+            tbl_read8_q2(dk_t + 4 * g, (const float *)(q_lds + kG * (kHD * 4 + 16) + 256 + 16 * kQiRow) + kSqRow * n,
                          dks, s0, s1);
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
