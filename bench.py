@@ -302,9 +302,13 @@ def decode_result(rd4, args, torch, name, graph=True):
     return {"value": value, "wall_ms": wall_ms, "roofline": roof, "config": info}, cpu, step
 
 
-def prefill_result(rd4, args, torch):
+def prefill_result(rd4, args, torch, one=True, chunks=True):
+    """cfg 5 as one call and as the reference engine's 8 calls of 512 queries
+    (one=False or chunks=False skips a half: profiling runs)."""
     step, dom, step_units, dom_units, cpu, info = build_workload(torch, rd4, "prefill", args)
     steps = max(1, min(args.steps, 50))
+    if not one:
+        step = dom = step.chunks
     wall_ms, dom_ms = measure(torch, step, dom, steps, min(args.warmup, 5))
     value = step_units / (wall_ms * 1e-3) / 1e12
     achieved = dom_units / (dom_ms * 1e-3) / 1e12
@@ -312,6 +316,9 @@ def prefill_result(rd4, args, torch):
             "unit": "TFLOP/s", "frac": round(achieved / F16_MFMA_PEAK_TFLOPS, 4),
             "traffic": measured_traffic("prefill"), "kernel_ms": round(dom_ms, 4)}
     # the same chunk as the reference engine issues it: 8 calls of 512 queries
+    if not chunks:
+        return {"value": round(value, 2), "unit": "TFLOP/s", "ms_per_step": round(wall_ms, 5),
+                "roofline": roof, "workload": "prefill" if one else "prefill_chunks"}, cpu
     ch_ms, _ = measure(torch, step.chunks, step.chunks, steps, min(args.warmup, 5))
     ch = step_units / (ch_ms * 1e-3) / 1e12
     chunked = {"calls": 8, "n_q_per_call": 512, "value": round(ch, 2), "unit": "TFLOP/s",
@@ -386,7 +393,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "decode_q8_0", "decode_f16", "decode_q4_0", "decode_q5_0_q4_1",
-                             "decode_tokens", "prefill", "copy", "read"])
+                             "decode_tokens", "prefill", "prefill_one", "prefill_chunks", "copy", "read"])
     ap.add_argument("--layers", type=int, default=16,
                     help="attention layers (each with its own cache) per decode step")
     ap.add_argument("--eager", action="store_true", help="launch the decode step eagerly, no graph")
@@ -431,6 +438,10 @@ def main():
                                        "kind": "port", "sample": sample2}
         return out
 
+    if args.workload in ("prefill_one", "prefill_chunks"):  # one half alone (profiling)
+        r, _ = prefill_result(rd4, args, torch, one=args.workload == "prefill_one", chunks=False)
+        print(json.dumps(r))
+        return
     if args.workload == "prefill":
         r, cpu = prefill_result(rd4, args, torch)
         res = dict(r, n_gpus=1, warmup=args.warmup, higher_is_better=True, scaling="weak",
