@@ -60,8 +60,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #ifndef RD4_DEC_ASM_WAIT
 #define RD4_DEC_ASM_WAIT 0
 #endif
+// Cache policy of the tile DMA (the load's aux bits): 2 = non-temporal, measured
+// faster for one token per CTA (q8_0 32K -1.5%, f16 32K -6%, q4_0 / q5_0 131K
+// within noise); pair mode keeps the default policy, its two token-pair CTAs of
+// a split read the same tiles (nt there: +5%).
 #ifndef RD4_DEC_AUX
-#define RD4_DEC_AUX 0
+#define RD4_DEC_AUX 2
 #endif
 // The ring's next tile is requested after the current tile's QK product
 // instead of before its wait: under a chip-wide burst of requests the DMA
@@ -938,6 +942,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       goff[r] = (uint32_t)(row * (int)vstride + 16 * swz<VT>(row, slot));
     }
   }
+  constexpr int kAux = PAIR ? 0 : RD4_DEC_AUX;
   auto issue = [&](int i) {  // i-th tile of this wave
     if (RD4_DEC_KNOBS && (a.dbg & 2048)) return;
     const int j0 = j_begin + tile_of(i) * j_step;
@@ -952,14 +957,14 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
                               : (lane + 64 * r < KCH ? kt0 : vt0);
         if (64 * r + 63 < KCH + VCH || lane + 64 * r < KCH + VCH)
           __builtin_amdgcn_global_load_lds((const void *)(base + goff[r]), (lds_void *)(st + 1024 * r),
-                                           16, 0, RD4_DEC_AUX);
+                                           16, 0, kAux);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < NI; ++r)
         if (64 * r + 63 < KCH + VCH || lane + 64 * r < KCH + VCH)
           __builtin_amdgcn_global_load_lds((const void *)src_of(r, nk, kt0, vt0),
-                                           (lds_void *)(st + 1024 * r), 16, 0, RD4_DEC_AUX);
+                                           (lds_void *)(st + 1024 * r), 16, 0, kAux);
     }
   };
   // The chunk's G query rows are copied into LDS once per CTA by the same
