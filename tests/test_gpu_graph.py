@@ -105,3 +105,49 @@ def test_epilogue_then_decode_in_graph(rd4, orc, dev):
         rd4.attn_decode(q, kc, vc, out, t, NH, NKV, HD, 1 / 16, 2, 2, gate=gate)
 
     _eager_vs_graph(torch, run, [out, gate, q], lambda: None)
+
+
+def test_prefill_key_splits_in_graph(rd4, orc, dev):
+    """A 512-query prefill_append call (key splits + merge launch, records in the
+    stream's library scratch) captured on a stream given its scratch by
+    rd4_stream_init: every replay equals the eager call on that stream."""
+    import ctypes
+    import torch
+    nh, nkv, hd, pos0, nq = NH, NKV, HD, 4096, 512
+    n = pos0 + nq
+    k = to_dev(orc.store_rows(1, orc.randn(n * nkv * hd, 701)), torch, dev)
+    v = to_dev(orc.store_rows(1, orc.randn(n * nkv * hd, 702)), torch, dev)
+    q = to_dev(orc.randn(nq * nh * hd, 703).reshape(nq, nh, hd).astype(np.float16), torch, dev)
+    g0 = to_dev(orc.randn(nq * nh * hd, 704).reshape(nq, nh, hd), torch, dev)
+    kn = to_dev(orc.randn(nq * nkv * hd, 705).reshape(nq, nkv, hd), torch, dev)
+    vn = to_dev(orc.randn(nq * nkv * hd, 706).reshape(nq, nkv, hd), torch, dev)
+    rb = rd4.kv_row_bytes(2, hd)
+    kq8 = torch.zeros(nq * nkv * rb, dtype=torch.uint8, device=dev)
+    vq8 = torch.zeros_like(kq8)
+    out = torch.full((nq, nh, hd), float("nan"), device=dev)
+    gate = g0.clone()
+    s = torch.cuda.Stream()
+    assert rd4.lib().rd4_stream_init(ctypes.c_void_p(s.cuda_stream)) == 0
+
+    def run():
+        rd4.prefill_append(q, k, v, out, pos0, nh, nkv, hd, 1 / 16, 1, 1, kn, vn, kq8, vq8, 2, gate=gate)
+
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        gate.copy_(g0)
+        run()
+    s.synchronize()
+    want = [out.clone(), gate.clone(), kq8.clone(), vq8.clone()]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run()
+    for i in range(3):
+        out.fill_(float("nan"))
+        kq8.zero_()
+        vq8.zero_()
+        gate.copy_(g0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, w in zip((out, gate, kq8, vq8), want):
+            assert torch.equal(o, w), "replay %d differs from the eager call" % i
