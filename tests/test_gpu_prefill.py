@@ -45,6 +45,31 @@ def test_fa2_entry_point(rd4, orc, dev):
     check_close(qd.cpu().numpy(), want, "fa2 in-place")
 
 
+def test_fa2_entry_point_reference_chunk(rd4, orc, dev):
+    """fa2_prefill_launch as graph.cuh calls it (n_q = 512, device positions,
+    q == out) at 2048 + 512 keys: the call takes the key-split path (64 row-block
+    CTAs on 256 CUs); sampled rows against the oracle, including the first and
+    last row of each 192-row CTA of kv head 0 and the chunk's last rows."""
+    import torch
+    nh, nkv, hd, pos0, nq = 24, 4, 256, 2048, 512
+    n = pos0 + nq
+    k = orc.store_rows(1, orc.randn(n * nkv * hd, 15))
+    v = orc.store_rows(1, orc.randn(n * nkv * hd, 16))
+    q = orc.randn(nq * nh * hd, 17).reshape(nq, nh, hd)
+    pos = np.arange(pos0, n, dtype=np.int32)
+    qd = to_dev(q, torch, dev)
+    rd4.fa2_prefill(qd, to_dev(k, torch, dev), to_dev(v, torch, dev), qd, to_dev(pos, torch, dev),
+                    n - 1, n, nh, nkv, hd, 1 / 16)
+    torch.cuda.synchronize()
+    got = qd.cpu().numpy()
+    grp = nh // nkv
+    rows = sorted({0, 1, nq - 2, nq - 1} | {min(nq - 1, (192 * c) // grp) for c in range(16)} |
+                  {min(nq - 1, (192 * c + 191) // grp) for c in range(16)})
+    rows = np.int32(rows)
+    want = orc.attn_batch(q[rows], k, v, pos[rows], nh, nkv, hd, 1 / 16, 1, 1, threads=8)
+    check_close(got[rows].ravel(), want, "fa2 512-query chunk (key splits) vs oracle")
+
+
 @pytest.mark.parametrize("nh,nkv,pos0,nq,q_f16,gated", [
     (24, 4, 0, 37, True, True),      # first chunk, ragged row count
     (16, 2, 50, 129, False, False),  # group 8, f32 queries, no gate
