@@ -547,10 +547,17 @@ void prefill_part(PrefillArgs &p, int kt, int vt, hipStream_t st) {
   const uintptr_t al = (uintptr_t)p.q | (uintptr_t)p.k | (uintptr_t)p.v | (uintptr_t)p.out | (uintptr_t)p.gate;
   if ((al & 15) || !prefill_mfma_supported(kt, vt, p.n_head, p.n_head_kv, p.head_dim)) return;
   const int s = prefill_ksplits(p);
+  if (s <= 1 || prefill_part_floats(p, s) > kPartialFloats) return;
+  // a stream without a set under graph capture runs unsplit: the lookup's
+  // failure is not the call's, so its message is not left behind
+  char saved[sizeof(g_err)];
+  std::memcpy(saved, g_err, sizeof(g_err));
   Scratch *sc = nullptr;
-  if (s > 1 && prefill_part_floats(p, s) <= kPartialFloats && get_scratch(st, &sc) == RD4_OK) {
+  if (get_scratch(st, &sc) == RD4_OK) {
     p.part = sc->partial_c;
     p.part_floats = kPartialFloats;
+  } else {
+    std::memcpy(g_err, saved, sizeof(g_err));
   }
 }
 
