@@ -60,10 +60,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #ifndef RD4_DEC_ASM_WAIT
 #define RD4_DEC_ASM_WAIT 0
 #endif
-// Cache policy of the tile DMA (the load's aux bits): 2 = non-temporal, measured
-// faster for one token per CTA (q8_0 32K -1.5%, f16 32K -6%, q4_0 / q5_0 131K
-// within noise); pair mode keeps the default policy, its two token-pair CTAs of
-// a split read the same tiles (nt there: +5%).
+// Cache policy of the tile DMA (the load's aux bits): 2 = non-temporal, for one
+// token per CTA over f16 / q8_0 caches (q8_0 32K -1.5%, f16 32K -6%). The
+// 4-bit types keep the default policy (nt there: time within noise, 13-15%
+// more fabric traffic: lines shared by neighbouring rows are fetched twice), and
+// so does pair mode, whose two token-pair CTAs of a split read the same tiles
+// (nt there: +5%).
 #ifndef RD4_DEC_AUX
 #define RD4_DEC_AUX 2
 #endif
@@ -942,7 +944,7 @@ __global__ __launch_bounds__((64 * TileShape<KT, VT>::WAVES), 1) void decode_mfm
       goff[r] = (uint32_t)(row * (int)vstride + 16 * swz<VT>(row, slot));
     }
   }
-  constexpr int kAux = PAIR ? 0 : RD4_DEC_AUX;
+  constexpr int kAux = (PAIR || !(KT == F16 || KT == Q8_0) || !(VT == F16 || VT == Q8_0)) ? 0 : RD4_DEC_AUX;
   auto issue = [&](int i) {  // i-th tile of this wave
     if (RD4_DEC_KNOBS && (a.dbg & 2048)) return;
     const int j0 = j_begin + tile_of(i) * j_step;
