@@ -357,10 +357,20 @@ def read_ceiling(rd4, args, torch, steps=None):
             rd4.read_probe(b, sink)
     run0 = as_graph(torch, step0) or step0
     floor_ms, _ = measure(torch, run0, run0, steps or args.steps, args.warmup)
-    return {"bytes_per_launch": nbytes, "launches_per_step": args.layers,
-            "us_per_launch": round(wall_ms * 1e3 / args.layers, 3), "GB/s": round(gbs, 1),
-            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "launch_floor_us": round(floor_ms * 1e3 / args.layers, 3)}
+    out = {"bytes_per_launch": nbytes, "launches_per_step": args.layers,
+           "us_per_launch": round(wall_ms * 1e3 / args.layers, 3), "GB/s": round(gbs, 1),
+           "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "launch_floor_us": round(floor_ms * 1e3 / args.layers, 3)}
+    # the probe's kernel duration from the committed rocprofv3 trace
+    # (profiles/read_probe_71mb.md): the ceiling without the launch cost
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            ns = json.load(f)["read"]["avg_ns_per_step"]
+        out["kernel_us_rocprof"] = round(ns / 1e3, 3)
+        out["kernel_frac_of_hbm_peak"] = round(nbytes / ns / HBM_PEAK_GBS, 4)
+    except (OSError, KeyError, ValueError):
+        pass
+    return out
 
 
 def build_workload(torch, rd4, name, args):
